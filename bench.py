@@ -1,0 +1,190 @@
+"""Benchmark of the BS-RoFormer transformer stack on one MI355X.
+
+Workload: one 17 s stereo chunk at 44.1 kHz (749,700 samples, n_fft 2048 / hop 441 -> 1701 frames),
+band-split into 62 bands of 256-d tokens, through the 24 sub-layers of the 12-block stack (time attention
++ FF, freq attention + FF) with seeded random weights.  A step is one whole stack forward on the chunk's
+tokens, resident in HBM (a device copy restores the input before each step, inside the timed region).
+
+Prints one JSON line: stack forwards/s, the time-attention kernel's TFLOP/s against the bf16 dense MFMA
+peak (measured with HIP events on the launch stream over the timed region), and a CPU baseline: the
+fp32 restructured torch path (the oracle) timed on the host's cores for one stack forward of the same
+chunk, whose output also gives the mask SNR of the GPU path.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "turbo-roformer_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+SAMPLES = 749_700  # 17 s at 44.1 kHz -> 1701 frames at hop 441
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def attn_flops(nseq: int, L: int) -> float:
+    """Algorithmic FLOPs of one attention call: QK^T and PV, 2*L*L*64 each, per (sequence, head)."""
+    return 4.0 * nseq * 8 * L * L * 64
+
+
+def tune_malloc() -> None:
+    """glibc: keep large blocks on the heap (the reference's tune_malloc, separator.py:32-54)."""
+    try:
+        import ctypes
+
+        libc = ctypes.CDLL("libc.so.6")
+        libc.mallopt(-4, 0)  # M_MMAP_MAX
+        libc.mallopt(-1, 2_000_000_000)  # M_TRIM_THRESHOLD
+    except (OSError, AttributeError):
+        pass
+
+
+def cpu_flags() -> set[str]:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    return set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and mask-SNR leg")
+    ap.add_argument("--seed", type=int, default=0)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the stack runs on a single MI355X (no multi-GPU path is built)",
+              file=sys.stderr)
+        return 2
+
+    from turbo_roformer_amd import _hip, signals, weights
+    from turbo_roformer_amd.host import HostPath
+    from turbo_roformer_amd.stack import HipStack
+
+    cfg = weights.RESURRECTION_CFG
+    sd = weights.init_state_dict(cfg, seed=a.seed, init="default", perturb=True)
+    host = HostPath(sd, cfg, "cpu")
+    raw = torch.from_numpy(signals.noise_mix(SAMPLES, seed=a.seed))[None]
+    X0 = host.band_split(host.spectrogram(raw))  # (1, T, F, 256) fp32
+    _, T, F, _ = X0.shape
+    stack = HipStack(sd, "cuda")
+    Xd0 = X0.reshape(-1, 256).contiguous().cuda()
+    X = torch.empty_like(Xd0)
+    nl = len(stack.layers)
+    nslot = len(_hip.SLOTS)
+
+    for _ in range(a.warmup):
+        X.copy_(Xd0)
+        stack(X, 1, T, F)
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nslot * nl)] for _ in range(a.steps)]
+    for evs in events:  # create the underlying events outside the timed region
+        for e in evs:
+            e.record()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(a.steps):
+        X.copy_(Xd0)
+        stack(X, 1, T, F, events=events[k])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / a.steps
+    print(f"bench: {a.steps} timed stack forwards, {ms:.3f} ms each", file=sys.stderr, flush=True)
+
+    per_kernel: dict[str, list[float]] = {}
+    for evs in events:
+        for i, mode in enumerate(stack.modes):
+            for s, name in enumerate(_hip.SLOTS):
+                key = f"{name}_{'t' if mode == 0 else 'f'}"
+                dt = evs[2 * (i * nslot + s)].elapsed_time(evs[2 * (i * nslot + s) + 1])
+                per_kernel.setdefault(key, []).append(dt)
+    kernel_ms = {k: float(np.mean(v)) for k, v in per_kernel.items()}
+    attn_t_ms = kernel_ms["attention_t"]
+    flops_t = attn_flops(F, T)
+    achieved = flops_t / (attn_t_ms * 1e-3) / 1e12
+
+    out_gpu = X.view(1, T, F, 256).cpu()
+    result = {
+        "metric": "17s-chunk stack forwards/sec; time-attn TFLOP/s and % of bf16 MFMA peak",
+        "value": round(1e3 / ms, 3),
+        "unit": "stack forwards/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian + pink-noise stereo mix, peak 0.5; seeded random weights)",
+        "config": {
+            "workload": "BS-RoFormer 12-block transformer stack (24 sub-layers) on one 17 s chunk",
+            "samples": SAMPLES, "frames": T, "bands": F, "tokens": T * F, "dim": 256, "heads": 8, "head_dim": 64,
+            "ff_hidden": 1024, "chunks": 1,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attention (time, 62 x 8 sequences of 1701 frames)",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "flops_per_launch": flops_t,
+            "avg_launch_ms": round(attn_t_ms, 4),
+        },
+        "kernels_ms_per_launch": {k: round(v, 4) for k, v in sorted(kernel_ms.items())},
+    }
+
+    if not a.no_cpu:
+        from oracle import folded, reference
+
+        tune_malloc()
+        threads = torch.get_num_threads()
+        layers = folded.fold(sd, cfg["depth"])
+        print(f"bench: cpu baseline, one fp32 stack forward on {threads} threads", file=sys.stderr, flush=True)
+        t2 = time.perf_counter()
+        ref = folded.stack(X0, layers)
+        t3 = time.perf_counter()
+        cpu_s = t3 - t2
+        snr_x = signals.snr_db(ref.numpy(), out_gpu.numpy())
+        m_ref = reference.mask_from_stack(ref, sd, cfg)
+        m_gpu = reference.mask_from_stack(out_gpu, sd, cfg)
+        snr_mask = signals.snr_db(m_ref.numpy(), m_gpu.numpy())
+        result["cpu_baseline"] = {
+            "value": round(1.0 / cpu_s, 5),
+            "unit": "stack forwards/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"one fp32 stack forward (24 sub-layers, {T}x{F} tokens) of the restructured torch path "
+                      f"(fast.py _transformer_torch restated), {cpu_s:.1f} s, avx512_bf16="
+                      f"{'avx512_bf16' in cpu_flags()}",
+            "gpu_speedup": round((1e3 / ms) * cpu_s, 1),
+        }
+        result["parity"] = {"mask_snr_db_vs_fp32": round(snr_mask, 2), "stack_out_snr_db_vs_fp32": round(snr_x, 2)}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,181 @@
+/*
+ * trf_hip.h - C ABI of the MI355X (gfx950) BS-RoFormer transformer stack.
+ *
+ * The library replaces the seven AVX512-BF16 torch ops of LoggeL/turbo-roformer
+ * (src/turbo_roformer/csrc/kernels.cpp:644-652) and the stack loop that calls them
+ * (FastBSRoformer._transformer_cpp, src/turbo_roformer/fast.py:269-341) with HIP
+ * kernels.  Every entry point takes plain device pointers, sizes and a HIP stream;
+ * no torch type appears in a signature.  The library allocates no memory and keeps
+ * no state beyond a thread-local error string: the caller owns every buffer.
+ *
+ * Shapes are fixed by the model: dim 256, 8 heads x 64, FF hidden 1024.
+ *
+ * Token order.  The residual stream X is fp32 [batch * T * F, 256] with token index
+ *     tok = (c * T + t) * F + f        (chunk c, frame t, band f)
+ * exactly as the reference keeps it (fast.py:378-380), extended by a chunk index c.
+ * Time attention (mode 0) runs over frames: batch*F sequences of length T.
+ * Frequency attention (mode 1) runs over bands: batch*T sequences of length F.
+ *
+ * Sequence buffers (written by trf_qkv_rope_gemm, read by trf_attention), bf16, with
+ * Lpad = trf_seq_pad(L) and sequence s, head h, position p, head feature d:
+ *     Q  [nseq][8][Lpad][64]   index ((s*8 + h)*Lpad + p)*64 + d   (rotated, scale folded)
+ *     K  [nseq][8][Lpad][64]   same index                         (rotated)
+ *     Vt [nseq][8][64][Lpad]   index ((s*8 + h)*64 + d)*Lpad + p   (transposed V)
+ * Positions p >= L are written as zeros.  G is fp32 [ntok][8] = sigmoid(gate logits).
+ *
+ * All bf16 values are passed as uint16_t bit patterns.  Error codes: 0 = ok; otherwise
+ * trf_last_error() returns a message for the calling thread.
+ */
+#ifndef TRF_HIP_H
+#define TRF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRF_ABI_VERSION 1
+
+#define TRF_DIM 256
+#define TRF_HEADS 8
+#define TRF_HEAD_DIM 64
+#define TRF_QKVG_ROWS 1544 /* q(8x64) | k(8x64) | v(8x64) | gate(8) */
+#define TRF_FF_HIDDEN 1024
+
+enum trf_status {
+  TRF_OK = 0,
+  TRF_ERR_ARG = 1,       /* bad argument: null pointer, misalignment, unsupported size */
+  TRF_ERR_WORKSPACE = 2, /* workspace smaller than trf_stack_workspace_bytes() */
+  TRF_ERR_HIP = 3        /* a HIP runtime call or kernel launch failed */
+};
+
+enum trf_mode { TRF_MODE_TIME = 0, TRF_MODE_FREQ = 1 };
+
+enum trf_dtype { TRF_F32 = 0, TRF_BF16 = 1 };
+
+/* Same type as hipStream_t; NULL is the default stream. */
+typedef struct ihipStream_t* trf_stream_t;
+
+/* Plain folded weights of one sub-layer (attention + feed-forward), device pointers,
+ * row-major [out][in].  This is what FastBSRoformer._prep builds (fast.py:163-191):
+ *   w_qkvg = [Wq * 16*g_attn / 8 ; Wk * 16*g_attn ; Wv * 16*g_attn ; Wgate * 16*g_attn]
+ *   w_ff1  = W1 * 16*g_ff
+ * (g = RMSNorm gamma, 16 = sqrt(256)), so every runtime norm is x / max(|x|, 1e-12). */
+typedef struct trf_layer_src {
+  const uint16_t* w_qkvg; /* bf16 [1544][256] */
+  const float* b_gate;    /* fp32 [8] */
+  const uint16_t* w_out;  /* bf16 [256][512] */
+  const uint16_t* w_ff1;  /* bf16 [1024][256] */
+  const float* b_ff1;     /* fp32 [1024] */
+  const uint16_t* w_ff2;  /* bf16 [256][1024] */
+  const float* b_ff2;     /* fp32 [256] */
+} trf_layer_src;
+
+/* ---------------------------------------------------------------- library */
+
+int trf_abi_version(void);
+const char* trf_last_error(void);
+
+/* Padded sequence length used by the Q/K/Vt buffers (multiple of 64). */
+int32_t trf_seq_pad(int32_t L);
+
+/* Element count (bf16) of one of Q, K or Vt for a mode and shape. */
+int64_t trf_seq_buffer_elems(int32_t mode, int32_t batch, int32_t T, int32_t F);
+
+/* ---------------------------------------------------------------- weights */
+
+/* Bytes of one packed sub-layer (all weights in the kernels' operand order). */
+size_t trf_layer_packed_bytes(void);
+
+/* Pack plain folded weights (device) into dst (device, trf_layer_packed_bytes()).
+ * Replaces the host-side VNNI packing _pack_w (fast.py:43-49) and _prep (fast.py:163-191). */
+int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream);
+
+/* ---------------------------------------------------------------- per-op entry points */
+
+/* X += Y (Y optional, f32 or bf16); out = X / max(|X|, eps) per row of 256.
+ * Replaces add_rmsnorm (kernels.cpp:101-137). */
+int trf_add_rmsnorm(float* X, const void* Y, int32_t y_dtype, void* out, int32_t out_dtype,
+                    int64_t n_rows, float eps, trf_stream_t stream);
+
+/* xn [ntok][256] bf16 -> Q, K, Vt (layouts above) and G = sigmoid(xn.Wg + b_gate).
+ * Rotary on q, k in fp32 from the accumulators with the caller's fp32 tables
+ * rope = [2][L][32] (cos then sin, angle = p * 10000^(-2i/64)).
+ * Replaces qkv_rope_gemm (kernels.cpp:439-540). */
+int trf_qkv_rope_gemm(const uint16_t* xn, const void* packed_layer, const float* rope, int32_t mode,
+                      int32_t batch, int32_t T, int32_t F, uint16_t* Q, uint16_t* K, uint16_t* Vt,
+                      float* G, trf_stream_t stream);
+
+/* Exact (two-pass, non-online) softmax attention per (sequence, head); epilogue
+ * O[tok][h*64 + d] = gate[tok][h] / rowsum * (P V)[.][d] in token order, bf16.
+ * Replaces attention (kernels.cpp:250-388). */
+int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
+                  uint16_t* O, int32_t mode, int32_t batch, int32_t T, int32_t F,
+                  trf_stream_t stream);
+
+/* X += A @ W^T (+ bias); xn = X / max(|X|, eps) as bf16.  which = 0: out-projection
+ * (A = O [n][512], no bias); which = 1: FF2 (A = H [n][1024], bias b_ff2).
+ * Replaces gemm_res_norm (kernels.cpp:542-586). */
+int trf_gemm_res_norm(const uint16_t* A, const void* packed_layer, int32_t which, float* X,
+                      uint16_t* xn, int64_t n_rows, float eps, trf_stream_t stream);
+
+/* H = gelu_erf(xn @ W1^T + b1), bf16 [n][1024].  Replaces gemm_gelu (kernels.cpp:609-642)
+ * and the oneDNN FF1 (fast.py:343-346). */
+int trf_gemm_gelu(const uint16_t* xn, const void* packed_layer, uint16_t* H, int64_t n_rows,
+                  trf_stream_t stream);
+
+/* ---------------------------------------------------------------- stack */
+
+/* Workspace bytes for trf_stack_forward / trf_attn_block / trf_ff_block at a shape. */
+size_t trf_stack_workspace_bytes(int32_t batch, int32_t T, int32_t F);
+
+/* The whole stack: one norm, then for each layer i (mode modes[i]):
+ *   qkv_rope_gemm, attention, out-proj + residual + norm, FF1 + GELU, FF2 + residual + norm.
+ * X fp32 [batch*T*F][256] is updated in place.  packed_layers is a host array of
+ * n_layers device pointers (trf_pack_layer output); modes is a host array.
+ * rope_time = [2][T][32], rope_freq = [2][F][32] fp32 device tables.
+ * Replaces FastBSRoformer._transformer_cpp (fast.py:269-341). */
+int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F,
+                      const void* const* packed_layers, const int32_t* modes, int32_t n_layers,
+                      const float* rope_time, const float* rope_freq, void* workspace,
+                      size_t workspace_bytes, trf_stream_t stream);
+
+/* Kernel slots of one layer in launch order (for trf_stack_forward_timed). */
+enum trf_kernel_slot {
+  TRF_SLOT_QKV = 0,
+  TRF_SLOT_ATTN = 1,
+  TRF_SLOT_OUT = 2,
+  TRF_SLOT_FF1 = 3,
+  TRF_SLOT_FF2 = 4,
+  TRF_SLOTS_PER_LAYER = 5
+};
+
+/* trf_stack_forward that also records caller-created hipEvent_t handles around kernels:
+ * events[2*(i*TRF_SLOTS_PER_LAYER + k)] before and events[... + 1] after kernel k of layer i,
+ * skipping NULL entries; n_events must be 0 or 2*TRF_SLOTS_PER_LAYER*n_layers.  This is the
+ * counterpart of the reference's per-section wall-clock profile (fast.py:62-80, 279-340). */
+int trf_stack_forward_timed(float* X, int32_t batch, int32_t T, int32_t F,
+                            const void* const* packed_layers, const int32_t* modes,
+                            int32_t n_layers, const float* rope_time, const float* rope_freq,
+                            void* workspace, size_t workspace_bytes, void* const* events,
+                            int32_t n_events, trf_stream_t stream);
+
+/* One attention sub-layer on the residual stream: xn = norm(X), qkv + rotary, attention,
+ * X += O @ Wout^T.  The counterpart of "x = attn(x) + x" (model.py:141) on the folded
+ * weights; rope is the table of this mode's axis. */
+int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer,
+                   int32_t mode, const float* rope, void* workspace, size_t workspace_bytes,
+                   trf_stream_t stream);
+
+/* One feed-forward sub-layer: X += W2 gelu(W1 norm(X) + b1) + b2 ("x = ff(x) + x",
+ * model.py:142). */
+int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer,
+                 void* workspace, size_t workspace_bytes, trf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRF_HIP_H */

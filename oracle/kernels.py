@@ -1,0 +1,134 @@
+"""bf16-rounding emulations of the reference's fused CPU ops, on the device layouts - test oracle.
+
+Each function reproduces where the reference kernels (src/turbo_roformer/csrc/kernels.cpp) round to
+bf16 and what they keep in fp32, with fp64 accumulation, so that a correct device kernel differs from
+it only by fp32 summation order (occasionally one bf16 step at a rounding boundary).  Inputs and outputs
+use the sequence-buffer layouts of include/trf_hip.h: Q, K [nseq, 8, Lpad, 64], Vt [nseq, 8, 64, Lpad]
+bf16, G [ntok, 8] fp32, tokens in (chunk, frame, band) order.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import reference
+
+Tensor = torch.Tensor
+H, DH, DIM, HID = 8, 64, 256, 1024
+LOG2E = 1.44269504088896341
+
+
+def seq_pad(L: int) -> int:
+    return (L + 63) // 64 * 64
+
+
+def token_index(mode: int, batch: int, T: int, F: int) -> Tensor:
+    """[nseq, L] token of position p in sequence s: time s=(c, f), p=t; freq s=(c, t), p=f (kernels.cpp:201)."""
+    tok = torch.arange(batch * T * F).view(batch, T, F)
+    if mode == 0:
+        return tok.permute(0, 2, 1).reshape(batch * F, T)
+    return tok.reshape(batch * T, F)
+
+
+def l2_rows(X: Tensor) -> Tensor:
+    return X / X.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+
+
+def add_rmsnorm(X: Tensor, Y: Tensor | None, out_dtype=torch.bfloat16) -> tuple[Tensor, Tensor]:
+    """add_rmsnorm (kernels.cpp:101-137): X' = X + Y; out = X' / max(|X'|, 1e-12)."""
+    Xn = X.float() + (Y.float() if Y is not None else 0.0)
+    out = (Xn.double() / Xn.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).to(out_dtype)
+    return Xn, out
+
+
+def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, batch: int, T: int, F: int):
+    """qkv_rope_gemm (kernels.cpp:439-540): fp32 accumulators, fp32 rotary of q and k, bf16 outputs,
+    fp32 sigmoid gates.  Returns Q, K, Vt (padded, zero pads) and G."""
+    n = xn.shape[0]
+    acc = (xn.double() @ W.double().t()).float()  # [n, 1544]
+    g = torch.sigmoid(acc[:, 3 * H * DH :].double() + b_gate.double()).float()
+    idx = token_index(mode, batch, T, F)
+    nseq, L = idx.shape
+    Lp = seq_pad(L)
+    ang = reference.rotary_angles(L, freqs)  # [L, 32]
+
+    def seq(part: int) -> Tensor:  # [nseq, H, L, DH] fp32
+        x = acc[:, part * H * DH : (part + 1) * H * DH].view(n, H, DH)
+        return x[idx].permute(0, 2, 1, 3)
+
+    q = reference.rotate(seq(0), ang).to(torch.bfloat16)
+    k = reference.rotate(seq(1), ang).to(torch.bfloat16)
+    v = seq(2).to(torch.bfloat16)
+    Q = torch.zeros(nseq, H, Lp, DH, dtype=torch.bfloat16)
+    K = torch.zeros_like(Q)
+    Vt = torch.zeros(nseq, H, DH, Lp, dtype=torch.bfloat16)
+    Q[:, :, :L] = q
+    K[:, :, :L] = k
+    Vt[:, :, :, :L] = v.transpose(-1, -2)
+    return Q, K, Vt, g
+
+
+def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int, T: int, F: int,
+              chunk: int = 64) -> Tensor:
+    """attention (kernels.cpp:250-388): exact row max over valid keys, e = 2^(s log2e - m log2e) in fp32,
+    unnormalised bf16 P, fp32 row sum of e, O = (P V) * gate / sum rounded to bf16, token order."""
+    idx = token_index(mode, batch, T, F)
+    nseq, L = idx.shape
+    O = torch.empty(batch * T * F, H * DH, dtype=torch.bfloat16)
+    for s0 in range(0, nseq, chunk):
+        s1 = min(nseq, s0 + chunk)
+        q = Q[s0:s1, :, :L].double()
+        k = K[s0:s1, :, :L].double()
+        v = Vt[s0:s1, :, :, :L].double().transpose(-1, -2)
+        S = (q @ k.transpose(-1, -2)).float()
+        m = S.amax(dim=-1, keepdim=True)
+        e = torch.exp2(S * LOG2E - m * LOG2E)  # fp32
+        rs = e.double().sum(dim=-1, keepdim=True)
+        o = e.to(torch.bfloat16).double() @ v  # [s, H, L, DH]
+        tok = idx[s0:s1]  # [s, L]
+        gate = G[tok].permute(0, 2, 1).unsqueeze(-1).double()  # [s, H, L, 1]
+        o = (o * (gate / rs)).to(torch.bfloat16)
+        O.view(-1, H, DH)[tok] = o.permute(0, 2, 1, 3)
+    return O
+
+
+def gemm_res_norm(A: Tensor, W: Tensor, bias: Tensor | None, X: Tensor) -> tuple[Tensor, Tensor]:
+    """gemm_res_norm (kernels.cpp:542-586): X' = X + A W^T (+ b) in fp32; xn = X'/|X'| as bf16."""
+    y = (A.double() @ W.double().t()).float() + X.float()
+    if bias is not None:
+        y = y + bias.float()
+    xn = (y.double() / y.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).to(torch.bfloat16)
+    return y, xn
+
+
+def gemm_gelu(xn: Tensor, W1: Tensor, b1: Tensor) -> Tensor:
+    """gemm_gelu (kernels.cpp:609-642) with the exact erf: H = gelu(xn W1^T + b1) as bf16."""
+    x = (xn.double() @ W1.double().t()).float() + b1.float()
+    return (0.5 * x.double() * (1.0 + torch.erf(x.double() / math.sqrt(2.0)))).to(torch.bfloat16)
+
+
+def bf16_weights(P: dict) -> dict:
+    """bf16 operands of one folded sub-layer (oracle.folded.fold output), as the kernels see them."""
+    return dict(
+        mode=P["mode"], W=P["W"][: 3 * H * DH + H].to(torch.bfloat16), b_gate=P["b"][3 * H * DH :].float(),
+        Wo=P["Wo"].to(torch.bfloat16), W1=P["W1"].to(torch.bfloat16), b1=P["b1"].float(),
+        W2=P["W2"].to(torch.bfloat16), b2=P["b2"].float(), freqs=P["freqs"],
+    )
+
+
+@torch.no_grad()
+def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int) -> Tensor:
+    """The fused-op sequence of ``_transformer_cpp`` (fast.py:269-341) with bf16 rounding at the same
+    points as the reference kernels; X is [batch*T*F, 256] fp32, returns a new tensor."""
+    X = X.float().clone()
+    _, xn = add_rmsnorm(X, None)
+    for P in layers:
+        w = bf16_weights(P)
+        Q, K, Vt, G = qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], w["mode"], batch, T, F)
+        O = attention(Q, K, Vt, G, w["mode"], batch, T, F)
+        X, xn = gemm_res_norm(O, w["Wo"], None, X)
+        Hh = gemm_gelu(xn, w["W1"], w["b1"])
+        X, xn = gemm_res_norm(Hh, w["W2"], w["b2"], X)
+    return X

@@ -1,0 +1,51 @@
+"""The C-ABI library loads without a GPU, exports every declared symbol, and validates arguments
+before touching the device."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from turbo_roformer_amd import _hip
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _hip.open_library()
+
+
+def test_exports_every_declared_function(lib):
+    names = _hip.header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(_hip._SIGNATURES), "ctypes signatures out of sync with trf_hip.h"
+
+
+def test_version_and_sizes(lib):
+    assert lib.trf_abi_version() == _hip.ABI_VERSION
+    assert [lib.trf_seq_pad(L) for L in (1, 62, 64, 65, 1700, 1701)] == [64, 64, 64, 128, 1728, 1728]
+    assert lib.trf_layer_packed_bytes() % 256 == 0
+    # Q/K/Vt elements: time 62 bands x 8 heads x 1728 x 64; freq 1701 frames x 8 x 64 x 64
+    assert lib.trf_seq_buffer_elems(0, 1, 1701, 62) == 62 * 8 * 1728 * 64
+    assert lib.trf_seq_buffer_elems(1, 1, 1701, 62) == 1701 * 8 * 64 * 64
+    ws = lib.trf_stack_workspace_bytes(1, 1701, 62)
+    n = 1701 * 62
+    assert ws >= n * (256 * 2 + 512 * 2 + 1024 * 2 + 8 * 4) + 3 * 1701 * 8 * 64 * 64 * 2
+    assert lib.trf_stack_workspace_bytes(29, 1701, 62) > 28 * ws
+
+
+def test_argument_errors_need_no_device(lib):
+    p = ctypes.c_void_p(256)  # aligned dummy pointer; argument checks reject before any launch
+    assert lib.trf_attention(p, p, p, p, p, 5, 1, 8, 2, None) == 1
+    assert b"mode" in lib.trf_last_error()
+    assert lib.trf_attention(p, p, p, p, None, 0, 1, 8, 2, None) == 1
+    assert b"O must not be NULL" in lib.trf_last_error()
+    assert lib.trf_qkv_rope_gemm(p, p, p, 0, 0, 8, 2, p, p, p, p, None) == 1
+    assert b"batch" in lib.trf_last_error()
+    assert lib.trf_gemm_res_norm(p, p, 3, p, p, 10, 1e-12, None) == 1
+    assert lib.trf_stack_forward(p, 1, 8, 2, None, None, 0, None, None, p, 0, None) == 2
+    assert b"workspace" in lib.trf_last_error()
+    assert lib.trf_seq_buffer_elems(2, 1, 8, 2) == -1
+    assert lib.trf_stack_workspace_bytes(0, 8, 2) == 0

@@ -1,0 +1,170 @@
+"""Per-op parity of the gfx950 kernels (through the C ABI) against the oracle's kernel emulations.
+
+Shapes cover both attention regimes (short L <= 64 single-pass, long L > 64 two-pass), odd and ragged
+lengths (one key past a 64-key tile, L = 1, the 1700/1701-frame chunk), batching, and the padded
+positions the kernels must zero.  Tolerance: within two bf16 steps elementwise (one rounding-boundary
+flip allowed in 1e-4 of the elements) and a per-op SNR floor.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import folded, kernels as ok
+from turbo_roformer_amd import _hip, weights
+from turbo_roformer_amd.stack import rope_table
+
+from .conftest import assert_bf16_close, rand_x, snr_db
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def layers(hip):
+    """Two folded sub-layers (time, freq) of a seeded model with N(0,0.02) weights and perturbed gains."""
+    cfg = dict(weights.TINY_CFG, depth=1)
+    sd = weights.init_state_dict(cfg, seed=3, init="normal")
+    out = []
+    for P in folded.fold(sd, 1):
+        w = ok.bf16_weights(P)
+        packed = torch.empty(_hip.layer_packed_bytes(), dtype=torch.uint8, device=DEV)
+        dev = dict(
+            w_qkvg=w["W"].to(DEV), b_gate=w["b_gate"].to(DEV), w_out=w["Wo"].to(DEV), w_ff1=w["W1"].to(DEV),
+            b_ff1=w["b1"].to(DEV), w_ff2=w["W2"].to(DEV), b_ff2=w["b2"].to(DEV),
+        )
+        _hip.pack_layer(**dev, out=packed)
+        out.append((w, packed))
+    torch.cuda.synchronize()
+    return out
+
+
+def _xn(n, seed):
+    return ok.l2_rows(rand_x(n, seed)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("y", [None, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_add_rmsnorm(hip, y, out_dtype):
+    n = 1003
+    X = rand_x(n, 1, 3.0)
+    Y = None if y is None else rand_x(n, 2).to(y)
+    ref_x, ref_out = ok.add_rmsnorm(X, Y, out_dtype)
+    Xd = X.to(DEV)
+    out = torch.empty(n, 256, dtype=out_dtype, device=DEV)
+    print(f"add_rmsnorm n={n} y={y} out={out_dtype}", flush=True)
+    _hip.add_rmsnorm(Xd, None if Y is None else Y.to(DEV), out)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(Xd.cpu(), ref_x, rtol=1e-6, atol=1e-6)
+    if out_dtype == torch.bfloat16:
+        assert_bf16_close(ref_out, out, "add_rmsnorm", min_snr=60)
+    else:
+        torch.testing.assert_close(out.cpu(), ref_out, rtol=1e-5, atol=1e-7)
+
+
+QKV_SHAPES = [  # (mode, batch, T, F)
+    (0, 1, 100, 7),
+    (1, 1, 100, 7),
+    (1, 2, 37, 62),
+    (0, 1, 65, 3),
+    (0, 1, 64, 3),
+    (0, 2, 1, 5),
+    (1, 1, 5, 1),
+    (0, 1, 1701, 2),
+    (1, 1, 9, 62),
+]
+
+
+@pytest.mark.parametrize("mode,batch,T,F", QKV_SHAPES)
+def test_qkv_rope_gemm(hip, layers, mode, batch, T, F):
+    w, packed = layers[mode]
+    n = batch * T * F
+    xn = _xn(n, 10 + T)
+    L = T if mode == 0 else F
+    rope = rope_table(w["freqs"], L)
+    Qr, Kr, Vr, Gr = ok.qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], mode, batch, T, F)
+    Q, K, Vt, G = _hip.seq_buffers(mode, batch, T, F)
+    for t in (Q, K, Vt):
+        t.fill_(1.0)  # pads must be overwritten with zeros
+    print(f"qkv_rope_gemm mode={mode} batch={batch} T={T} F={F}", flush=True)
+    _hip.qkv_rope_gemm(xn.to(DEV), packed, rope.to(DEV), mode, batch, T, F, Q, K, Vt, G)
+    torch.cuda.synchronize()
+    assert_bf16_close(Qr, Q, "Q")
+    assert_bf16_close(Kr, K, "K")
+    assert_bf16_close(Vr, Vt, "Vt")
+    torch.testing.assert_close(G.cpu(), Gr, rtol=2e-5, atol=2e-6)
+    assert (Q.cpu()[:, :, L:] == 0).all() and (K.cpu()[:, :, L:] == 0).all() and (Vt.cpu()[..., L:] == 0).all()
+
+
+ATT_SHAPES = QKV_SHAPES + [(0, 1, 1700, 2), (0, 1, 200, 9), (1, 3, 11, 64)]
+
+
+@pytest.mark.parametrize("mode,batch,T,F", ATT_SHAPES)
+def test_attention(hip, layers, mode, batch, T, F):
+    w, _ = layers[mode]
+    n = batch * T * F
+    # sharper attention than unit-norm inputs give: scale xn so scores span tens of units
+    xn = (ok.l2_rows(rand_x(n, 20 + T)) * 1.0).to(torch.bfloat16)
+    Wq = w["W"].float().clone()
+    Wq[:1024] *= 6.0
+    Q, K, Vt, G = ok.qkv_rope(xn, Wq.to(torch.bfloat16), w["b_gate"], w["freqs"], mode, batch, T, F)
+    Oref = ok.attention(Q, K, Vt, G, mode, batch, T, F)
+    O = torch.empty(n, 512, dtype=torch.bfloat16, device=DEV)
+    print(f"attention mode={mode} batch={batch} T={T} F={F}", flush=True)
+    _hip.attention(Q.to(DEV), K.to(DEV), Vt.to(DEV), G.to(DEV), O, mode, batch, T, F)
+    torch.cuda.synchronize()
+    assert_bf16_close(Oref, O, "O", min_snr=48)
+    # against textbook fp64 softmax attention on the same bf16 operands (no bf16 P): SNR only
+    L = T if mode == 0 else F
+    idx = ok.token_index(mode, batch, T, F)
+    q, k = Q[:, :, :L].double(), K[:, :, :L].double()
+    v = Vt[:, :, :, :L].double().transpose(-1, -2)
+    o = torch.softmax(q @ k.transpose(-1, -2), dim=-1) @ v
+    o = o * G[idx].permute(0, 2, 1).unsqueeze(-1).double()
+    exact = torch.empty(n, 8, 64, dtype=torch.float64)
+    exact[idx] = o.permute(0, 2, 1, 3)
+    assert snr_db(exact.view(n, 512).numpy(), O.double().cpu().numpy()) >= 40.0
+
+
+@pytest.mark.parametrize("which", [0, 1])
+@pytest.mark.parametrize("n", [1, 31, 1000, 4133])
+def test_gemm_res_norm(hip, layers, which, n):
+    w, packed = layers[0]
+    kd = 512 if which == 0 else 1024
+    A = (rand_x(n, 30 + n).repeat(1, kd // 256) * 0.5).to(torch.bfloat16)
+    X = rand_x(n, 40 + n, 2.0)
+    Xr, xnr = ok.gemm_res_norm(A, w["Wo"] if which == 0 else w["W2"], None if which == 0 else w["b2"], X)
+    Xd = X.to(DEV)
+    xn = torch.empty(n, 256, dtype=torch.bfloat16, device=DEV)
+    print(f"gemm_res_norm which={which} n={n}", flush=True)
+    _hip.gemm_res_norm(A.to(DEV), packed, which, Xd, xn)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(Xd.cpu(), Xr, rtol=1e-5, atol=1e-5)
+    assert_bf16_close(xnr, xn, "xn", min_snr=55)
+
+
+@pytest.mark.parametrize("n", [1, 77, 4096])
+def test_gemm_gelu(hip, layers, n):
+    w, packed = layers[1]
+    xn = _xn(n, 50 + n)
+    Hr = ok.gemm_gelu(xn, w["W1"], w["b1"])
+    H = torch.empty(n, 1024, dtype=torch.bfloat16, device=DEV)
+    print(f"gemm_gelu n={n}", flush=True)
+    _hip.gemm_gelu(xn.to(DEV), packed, H)
+    torch.cuda.synchronize()
+    assert_bf16_close(Hr, H, "H", min_snr=50)
+
+
+def test_errors_are_raised(hip, layers):
+    """Bad arguments come back as RuntimeError with the library's message (no launch)."""
+    w, packed = layers[0]
+    Q, K, Vt, G = _hip.seq_buffers(0, 1, 8, 2)
+    O = torch.empty(16, 512, dtype=torch.bfloat16, device=DEV)
+    lib = _hip.load()
+    rc = lib.trf_attention(Q.data_ptr(), K.data_ptr(), Vt.data_ptr(), G.data_ptr(), O.data_ptr(), 7, 1, 8, 2, None)
+    assert rc == 1 and b"mode" in lib.trf_last_error()
+    rc = lib.trf_attention(Q.data_ptr() + 2, K.data_ptr(), Vt.data_ptr(), G.data_ptr(), O.data_ptr(), 0, 1, 8, 2, None)
+    assert rc == 1 and b"aligned" in lib.trf_last_error()
+    with pytest.raises(ValueError):
+        _hip.attention(Q, K, Vt, G, O[:8], 0, 1, 8, 2)

@@ -1,0 +1,105 @@
+"""Whole-stack parity of the gfx950 path against the oracle, and full-size invariants.
+
+* tiny model (4 sub-layers) on band-split tokens of synthetic audio: HIP vs the fp32 reference forward
+  semantics (mask SNR >= 55 dB) and vs the bf16 kernel emulation (tight);
+* odd frame counts (T = 4 from a 385-sample clip, T = 40) and a 2-chunk batch that must equal the
+  chunks run one at a time (bitwise);
+* the full 17 s chunk shape (T = 1701, F = 62) for one time and one freq sub-layer: the band/frame
+  permutation equivariance of each axial pass, bitwise.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import folded, kernels as ok, reference
+from turbo_roformer_amd import signals, weights
+from turbo_roformer_amd.stack import HipStack
+
+from .conftest import snr_db
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+CFG = weights.TINY_CFG
+
+
+def _tokens(sd, n, seed, batch=1):
+    raw = torch.stack([torch.from_numpy(signals.noise_mix(n, seed=seed + i)) for i in range(batch)])
+    X = reference.stack_input(raw, sd, CFG)  # (b, T, F, 256)
+    return raw, X
+
+
+@pytest.fixture(scope="module")
+def stack(hip, tiny_sd):
+    return HipStack(tiny_sd, DEV)
+
+
+@pytest.mark.parametrize("n", [weights.TINY_HOP * (weights.TINY_DIM_T - 1), 385, 5000])
+def test_stack_matches_reference(stack, tiny_sd, n):
+    raw, X = _tokens(tiny_sd, n, seed=n)
+    b, T, F, _ = X.shape
+    ref = reference.stack(X, tiny_sd, CFG["depth"])
+    emu = ok.stack(X.reshape(-1, 256), folded.fold(tiny_sd, CFG["depth"]), b, T, F)
+    Xd = X.reshape(-1, 256).contiguous().to(DEV)
+    print(f"stack tiny n={n} T={T} F={F}", flush=True)
+    stack(Xd, b, T, F)
+    torch.cuda.synchronize()
+    out = Xd.cpu()
+    s_ref = snr_db(ref.reshape(-1, 256).numpy(), out.numpy())
+    s_emu = snr_db(emu.numpy(), out.numpy())
+    m_ref = reference.mask_from_stack(ref, tiny_sd, CFG)
+    m_hip = reference.mask_from_stack(out.view(b, T, F, 256), tiny_sd, CFG)
+    s_mask = snr_db(m_ref.numpy(), m_hip.numpy())
+    m_emu = reference.mask_from_stack(emu.view(b, T, F, 256), tiny_sd, CFG)
+    s_mask_emu = snr_db(m_ref.numpy(), m_emu.numpy())
+    print(f"  X snr vs fp32 {s_ref:.1f} dB, vs bf16 emulation {s_emu:.1f} dB; "
+          f"mask snr {s_mask:.1f} dB (emulation of the reference kernels: {s_mask_emu:.1f} dB)")
+    # as accurate as the reference's bf16 kernel design on the same input, and well above its 40 dB bar
+    assert s_mask >= s_mask_emu - 1.0
+    assert s_mask >= 50.0
+    assert s_ref >= 45.0
+    assert s_emu >= 55.0
+
+
+def test_batched_chunks_equal_single(stack, tiny_sd):
+    _, X = _tokens(tiny_sd, 40 * weights.TINY_HOP, seed=7, batch=2)
+    b, T, F, _ = X.shape
+    Xb = X.reshape(-1, 256).contiguous().to(DEV)
+    print(f"stack batch=2 T={T} F={F}", flush=True)
+    stack(Xb, b, T, F)
+    singles = []
+    for i in range(b):
+        Xi = X[i].reshape(-1, 256).contiguous().to(DEV)
+        stack(Xi, 1, T, F)
+        singles.append(Xi)
+    torch.cuda.synchronize()
+    assert torch.equal(Xb.view(b, -1, 256), torch.stack(singles).view(b, -1, 256))
+
+
+@pytest.fixture(scope="module")
+def full_stack(hip):
+    cfg = dict(weights.RESURRECTION_CFG, depth=1)
+    sd = weights.init_state_dict(cfg, seed=11, init="normal")
+    return HipStack(sd, DEV)
+
+
+@pytest.mark.parametrize("layer,axis", [(0, 2), (1, 1)])
+def test_full_size_axial_equivariance(full_stack, layer, axis):
+    """Time attention (layer 0) treats bands as independent sequences, freq attention (layer 1) frames:
+    permuting that axis of the input permutes the output, bit for bit, at T = 1701, F = 62."""
+    T, F = 1701, 62
+    g = torch.Generator().manual_seed(5)
+    X = torch.randn(1, T, F, 256, generator=g)
+    perm = torch.randperm(X.shape[axis], generator=g)
+    Xa = X.reshape(-1, 256).contiguous().to(DEV)
+    Xb = X.index_select(axis, perm).reshape(-1, 256).contiguous().to(DEV)
+    print(f"full-size equivariance layer={layer}", flush=True)
+    full_stack.attn_block(Xa, 1, T, F, layer)
+    full_stack.ff_block(Xa, 1, T, F, layer)
+    full_stack.attn_block(Xb, 1, T, F, layer)
+    full_stack.ff_block(Xb, 1, T, F, layer)
+    torch.cuda.synchronize()
+    a = Xa.view(1, T, F, 256).cpu().index_select(axis, perm)
+    assert torch.equal(a, Xb.view(1, T, F, 256).cpu())
+    assert torch.isfinite(a).all()

@@ -1,0 +1,158 @@
+"""Pins of the oracle itself: closed forms, library routines, brute force, invariants, folding, and
+the reference's own known answers.  Each check is chosen so that a plausible slip (wrong sign or pair
+layout in the rotary, a dropped 1/sqrt(d), a transposed axis) fails it."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import folded, kernels as ok, reference
+from turbo_roformer_amd import weights
+
+from .conftest import snr_db
+
+CFG = weights.TINY_CFG
+
+
+def test_rms_norm_closed_form():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 256, generator=g, dtype=torch.float64)
+    gamma = 1 + 0.25 * torch.randn(256, generator=g, dtype=torch.float64)
+    y = reference.rms_norm(x, gamma)
+    torch.testing.assert_close(y, F.normalize(x, dim=-1) * 16.0 * gamma)
+    torch.testing.assert_close((y / gamma).norm(dim=-1), torch.full((5,), 16.0, dtype=torch.float64))
+    assert torch.equal(reference.rms_norm(torch.zeros(1, 4), torch.ones(4)), torch.zeros(1, 4))  # eps on the norm
+
+
+def test_rotary_is_a_complex_rotation_of_interleaved_pairs():
+    g = torch.Generator().manual_seed(1)
+    L, d = 9, 64
+    t = torch.randn(2, L, d, generator=g, dtype=torch.float64)
+    freqs = weights.rotary_freqs().double()
+    ang = torch.arange(L, dtype=torch.float64)[:, None] * freqs[None, :]
+    out = reference.rotate(t, ang)
+    z = torch.complex(t[..., 0::2], t[..., 1::2]) * torch.polar(torch.ones_like(ang), ang)
+    torch.testing.assert_close(out[..., 0::2], z.real)
+    torch.testing.assert_close(out[..., 1::2], z.imag)
+    torch.testing.assert_close(out[:, 0], t[:, 0])  # position 0 is the identity
+    # pairs keep their length, and q.k depends only on the position difference
+    torch.testing.assert_close(out.view(2, L, 32, 2).norm(dim=-1), t.view(2, L, 32, 2).norm(dim=-1))
+    q = torch.randn(d, generator=g, dtype=torch.float64).expand(L, d)
+    k = torch.randn(d, generator=g, dtype=torch.float64).expand(L, d)
+    rq, rk = reference.rotate(q, ang), reference.rotate(k, ang)
+    torch.testing.assert_close(rq[2] @ rk[5], rq[4] @ rk[7])
+    assert not torch.allclose(rq[2] @ rk[5], rq[2] @ rk[6])
+
+
+def test_rotary_frequencies():
+    f = weights.rotary_freqs()
+    ref = torch.tensor([10000.0 ** (-2 * i / 64) for i in range(32)], dtype=torch.float64)
+    torch.testing.assert_close(f.double(), ref, rtol=2e-7, atol=0)
+    assert f.dtype == torch.float32 and f[0] == 1.0
+
+
+def test_softmax_attention_vs_sdpa_and_brute_force():
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(2, 3, 7, 16, generator=g, dtype=torch.float64) for _ in range(3))
+    out = reference.softmax_attention(q, k, v, 0.25)
+    torch.testing.assert_close(out, F.scaled_dot_product_attention(q, k, v, scale=0.25))
+    b, h, i = 1, 2, 4
+    w = [math.exp(0.25 * float(q[b, h, i] @ k[b, h, j])) for j in range(7)]
+    brute = sum(wj * v[b, h, j] for j, wj in enumerate(w)) / sum(w)
+    torch.testing.assert_close(out[b, h, i], brute)
+
+
+def test_gelu_is_the_erf_form():
+    x = torch.linspace(-6, 6, 97, dtype=torch.float64)
+    ref = torch.tensor([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x.tolist()], dtype=torch.float64)
+    torch.testing.assert_close(reference.gelu_erf(x), ref)
+    assert (reference.gelu_erf(x) - F.gelu(x, approximate="tanh")).abs().max() > 1e-5  # not the tanh form
+
+
+def test_token_index_known_answers():
+    # time: sequence (c, f), position t -> (c*T + t)*F + f ; freq: sequence (c, t), position f
+    assert ok.token_index(0, 2, 3, 2).tolist() == [[0, 2, 4], [1, 3, 5], [6, 8, 10], [7, 9, 11]]
+    assert ok.token_index(1, 1, 3, 2).tolist() == [[0, 1], [2, 3], [4, 5]]
+
+
+@pytest.fixture(scope="module")
+def tiny_tokens(tiny_sd):
+    from turbo_roformer_amd import signals
+
+    raw = torch.from_numpy(signals.noise_mix(12 * 128, seed=3))[None]
+    return raw, reference.stack_input(raw, tiny_sd, CFG)
+
+
+def test_folded_stack_equals_reference(tiny_sd, tiny_tokens):
+    _, X = tiny_tokens
+    ref = reference.stack(X.double(), {k: v.double() for k, v in tiny_sd.items()}, CFG["depth"])
+    fp32 = reference.stack(X, tiny_sd, CFG["depth"])
+    fo = folded.stack(X, folded.fold(tiny_sd, CFG["depth"]))
+    assert snr_db(ref.numpy(), fp32.numpy()) >= 100.0
+    assert snr_db(ref.numpy(), fo.numpy()) >= 100.0
+
+
+def test_kernel_emulation_close_to_reference(tiny_sd, tiny_tokens):
+    _, X = tiny_tokens
+    b, T, F_, _ = X.shape
+    ref = reference.stack(X, tiny_sd, CFG["depth"])
+    emu = ok.stack(X.reshape(-1, 256), folded.fold(tiny_sd, CFG["depth"]), b, T, F_)
+    s = snr_db(ref.reshape(-1, 256).numpy(), emu.numpy())
+    assert 35.0 <= s < 100.0, s  # bf16 operands: close, but visibly not fp32
+
+
+def test_axial_passes_group_the_right_axis(tiny_sd, tiny_tokens):
+    """Time transformer: bands are independent sequences; freq transformer: frames are."""
+    _, X = tiny_tokens
+    b, T, F_, d = X.shape
+    perm = torch.randperm(F_, generator=torch.Generator().manual_seed(0))
+    xt = X.transpose(1, 2).reshape(b * F_, T, d)
+    yt = reference.transformer(xt, tiny_sd, "layers.0.0")
+    yp = reference.transformer(xt[perm], tiny_sd, "layers.0.0")
+    torch.testing.assert_close(yp, yt[perm])
+    # positions matter along the attended axis: reversing frames is not equivariant
+    assert not torch.allclose(reference.transformer(xt.flip(1), tiny_sd, "layers.0.0").flip(1), yt, atol=1e-4)
+
+
+def test_forward_output_length(tiny_sd):
+    raw = torch.randn(1, 2, 5000, generator=torch.Generator().manual_seed(0))
+    assert reference.forward(raw, tiny_sd, CFG).shape == (1, 2, 128 * (5000 // 128))
+
+
+def test_emulated_attention_rows_and_gate():
+    """With V = identity-like one-hot rows the emulated output is the bf16 softmax row times the gate."""
+    g = torch.Generator().manual_seed(4)
+    batch, T, F_ = 1, 5, 1
+    Q = torch.zeros(1, 8, 64, 64, dtype=torch.bfloat16)
+    K = torch.zeros_like(Q)
+    Vt = torch.zeros(1, 8, 64, 64, dtype=torch.bfloat16)
+    Q[:, :, :5] = torch.randn(1, 8, 5, 64, generator=g).to(torch.bfloat16)
+    K[:, :, :5] = torch.randn(1, 8, 5, 64, generator=g).to(torch.bfloat16)
+    for j in range(5):
+        Vt[:, :, j, j] = 1.0
+    G = torch.rand(5, 8, generator=g)
+    O = ok.attention(Q, K, Vt, G, 0, batch, T, F_).float().view(5, 8, 64)
+    p = torch.softmax(Q[0, :, :5].double() @ K[0, :, :5].double().transpose(-1, -2), -1)  # [8, 5, 5]
+    torch.testing.assert_close(O[:, :, :5], (p * G.t().double()[:, :, None]).permute(1, 0, 2).float(), rtol=1e-2, atol=2e-3)
+    torch.testing.assert_close(O.sum(-1), G, rtol=2e-2, atol=0)
+    assert (O[:, :, 5:] == 0).all()
+
+
+def test_kernel_emulation_pads_and_layouts():
+    g = torch.Generator().manual_seed(6)
+    n, T, F_ = 2 * 3 * 70, 3, 70
+    xn = torch.randn(n, 256, generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(1544, 256, generator=g)).to(torch.bfloat16)
+    Q, K, Vt, G = ok.qkv_rope(xn, W, torch.zeros(8), weights.rotary_freqs(), 1, 2, T, F_)
+    assert Q.shape == (6, 8, 128, 64) and Vt.shape == (6, 8, 64, 128)
+    assert (Q[:, :, 70:] == 0).all() and (Vt[..., 70:] == 0).all()
+    # V of token (c=1, t=2, f=5) lands in sequence c*T+t = 5 at position 5, transposed, un-rotated
+    tok = (1 * T + 2) * F_ + 5
+    v = (xn[tok].double() @ W[1024:1536].double().t()).float().to(torch.bfloat16).view(8, 64)
+    assert torch.equal(Vt[5, :, :, 5], v)
+    np.testing.assert_allclose(G[tok].numpy(), torch.sigmoid(xn[tok].double() @ W[1536:].double().t()).numpy(), rtol=1e-6)

@@ -1,0 +1,333 @@
+// C ABI of the stack (declared in include/trf_hip.h): argument checks, workspace layout and
+// the 24-sub-layer driver.  Host code only; the kernels live in trf_kernels.hip.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "trf_hip.h"
+#include "trf_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TRF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return TRF_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_shape(int32_t batch, int32_t T, int32_t F) {
+  if (batch < 1 || T < 1 || F < 1) return fail(TRF_ERR_ARG, "batch, T and F must be >= 1 (got %d, %d, %d)", batch, T, F);
+  if (int64_t(batch) * T * F >= (int64_t(1) << 31))
+    return fail(TRF_ERR_ARG, "batch*T*F = %lld tokens is too large", (long long)batch * T * F);
+  return TRF_OK;
+}
+
+int check_mode(int32_t mode) {
+  if (mode != TRF_MODE_TIME && mode != TRF_MODE_FREQ) return fail(TRF_ERR_ARG, "mode must be 0 (time) or 1 (freq), got %d", mode);
+  return TRF_OK;
+}
+
+#define TRF_REQUIRE(ptr, name)                                                          \
+  do {                                                                                  \
+    if (!(ptr)) return fail(TRF_ERR_ARG, "%s must not be NULL", name);                  \
+    if (!aligned((ptr), 16)) return fail(TRF_ERR_ARG, "%s must be 16-byte aligned", name); \
+  } while (0)
+
+struct Workspace {
+  uint16_t* xn;
+  uint16_t* O;
+  uint16_t* H;
+  float* G;
+  uint16_t* Q;
+  uint16_t* K;
+  uint16_t* Vt;
+  size_t bytes;
+};
+
+size_t round_up(size_t x) { return (x + 255) / 256 * 256; }
+
+int64_t seq_elems(int mode, int batch, int T, int F) {
+  const trf::SeqShape s = trf::seq_shape(mode, batch, T, F);
+  return int64_t(s.nseq) * trf::kHeads * s.Lpad * trf::kHeadDim;
+}
+
+Workspace plan(int32_t batch, int32_t T, int32_t F, uint8_t* base) {
+  const size_t n = size_t(batch) * T * F;
+  const int64_t seq = seq_elems(0, batch, T, F) > seq_elems(1, batch, T, F) ? seq_elems(0, batch, T, F)
+                                                                            : seq_elems(1, batch, T, F);
+  Workspace w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += round_up(bytes);
+    return p;
+  };
+  w.xn = reinterpret_cast<uint16_t*>(take(n * trf::kDim * 2));
+  w.O = reinterpret_cast<uint16_t*>(take(n * 512 * 2));
+  w.H = reinterpret_cast<uint16_t*>(take(n * trf::kHidden * 2));
+  w.G = reinterpret_cast<float*>(take(n * trf::kHeads * 4));
+  w.Q = reinterpret_cast<uint16_t*>(take(size_t(seq) * 2));
+  w.K = reinterpret_cast<uint16_t*>(take(size_t(seq) * 2));
+  w.Vt = reinterpret_cast<uint16_t*>(take(size_t(seq) * 2));
+  w.bytes = off;
+  return w;
+}
+
+hipStream_t as_hip(trf_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Optional event pair around each kernel of a layer (profiling); events == nullptr disables it.
+struct Events {
+  void* const* ev = nullptr;
+  int layer = 0;
+  int record(int slot, int end, hipStream_t st) const {
+    if (!ev) return TRF_OK;
+    void* e = ev[2 * (layer * TRF_SLOTS_PER_LAYER + slot) + end];
+    if (!e) return TRF_OK;
+    const hipError_t rc = hipEventRecord(reinterpret_cast<hipEvent_t>(e), st);
+    if (rc != hipSuccess) return fail(TRF_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(rc));
+    return TRF_OK;
+  }
+};
+
+#define TRF_TRY(expr)              \
+  do {                             \
+    if (int rc_ = (expr)) return rc_; \
+  } while (0)
+
+// One attention sub-layer on an already normalised xn: qkv, attention, out-proj + residual + norm.
+int run_attn(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
+             int64_t n, hipStream_t st, const Events& ev = Events{}) {
+  TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
+  trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
+  TRF_TRY(check_launch("qkv_rope_gemm"));
+  TRF_TRY(ev.record(TRF_SLOT_QKV, 1, st));
+  TRF_TRY(ev.record(TRF_SLOT_ATTN, 0, st));
+  trf::launch_attention(w.Q, w.K, w.Vt, w.G, w.O, sh, st);
+  TRF_TRY(check_launch("attention"));
+  TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
+  TRF_TRY(ev.record(TRF_SLOT_OUT, 0, st));
+  trf::launch_gemm_res_norm(w.O, layer, 0, X, w.xn, n, 1e-12f, st);
+  TRF_TRY(check_launch("gemm_res_norm(out)"));
+  return ev.record(TRF_SLOT_OUT, 1, st);
+}
+
+int run_ff(float* X, const uint8_t* layer, const Workspace& w, int64_t n, hipStream_t st,
+           const Events& ev = Events{}) {
+  TRF_TRY(ev.record(TRF_SLOT_FF1, 0, st));
+  trf::launch_gemm_gelu(w.xn, layer, w.H, n, st);
+  TRF_TRY(check_launch("gemm_gelu"));
+  TRF_TRY(ev.record(TRF_SLOT_FF1, 1, st));
+  TRF_TRY(ev.record(TRF_SLOT_FF2, 0, st));
+  trf::launch_gemm_res_norm(w.H, layer, 1, X, w.xn, n, 1e-12f, st);
+  TRF_TRY(check_launch("gemm_res_norm(ff2)"));
+  return ev.record(TRF_SLOT_FF2, 1, st);
+}
+
+int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers, const int32_t* modes,
+               int32_t n_layers, const float* rope_time, const float* rope_freq, void* workspace,
+               size_t workspace_bytes, void* const* events, int32_t n_events, hipStream_t st) {
+  TRF_TRY(check_shape(batch, T, F));
+  TRF_REQUIRE(X, "X");
+  TRF_REQUIRE(workspace, "workspace");
+  if (n_layers < 0) return fail(TRF_ERR_ARG, "n_layers must be >= 0");
+  if (n_layers > 0 && (!packed_layers || !modes)) return fail(TRF_ERR_ARG, "packed_layers and modes must not be NULL");
+  if (n_events != 0 && (n_events != 2 * TRF_SLOTS_PER_LAYER * n_layers || !events))
+    return fail(TRF_ERR_ARG, "n_events must be 0 or 2*%d*n_layers with a non-NULL array", TRF_SLOTS_PER_LAYER);
+  for (int32_t i = 0; i < n_layers; ++i) {
+    TRF_TRY(check_mode(modes[i]));
+    TRF_REQUIRE(packed_layers[i], "packed_layers[i]");
+    if (modes[i] == TRF_MODE_TIME) TRF_REQUIRE(rope_time, "rope_time");
+    if (modes[i] == TRF_MODE_FREQ) TRF_REQUIRE(rope_freq, "rope_freq");
+  }
+  const Workspace w = plan(batch, T, F, static_cast<uint8_t*>(workspace));
+  if (workspace_bytes < w.bytes)
+    return fail(TRF_ERR_WORKSPACE, "workspace is %zu bytes, need %zu", workspace_bytes, w.bytes);
+  const int64_t n = int64_t(batch) * T * F;
+  trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
+  TRF_TRY(check_launch("add_rmsnorm"));
+  for (int32_t i = 0; i < n_layers; ++i) {
+    const uint8_t* layer = static_cast<const uint8_t*>(packed_layers[i]);
+    const trf::SeqShape sh = trf::seq_shape(modes[i], batch, T, F);
+    Events ev;
+    ev.ev = n_events ? events : nullptr;
+    ev.layer = i;
+    TRF_TRY(run_attn(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, st, ev));
+    TRF_TRY(run_ff(X, layer, w, n, st, ev));
+  }
+  return TRF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int trf_abi_version(void) { return TRF_ABI_VERSION; }
+
+const char* trf_last_error(void) { return g_err.c_str(); }
+
+int32_t trf_seq_pad(int32_t L) { return trf::seq_pad(L); }
+
+int64_t trf_seq_buffer_elems(int32_t mode, int32_t batch, int32_t T, int32_t F) {
+  if (check_mode(mode) || check_shape(batch, T, F)) return -1;
+  return seq_elems(mode, batch, T, F);
+}
+
+size_t trf_layer_packed_bytes(void) { return trf::kLayerBytes; }
+
+int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream) {
+  if (!src) return fail(TRF_ERR_ARG, "src must not be NULL");
+  TRF_REQUIRE(dst, "dst");
+  TRF_REQUIRE(src->w_qkvg, "w_qkvg");
+  TRF_REQUIRE(src->w_out, "w_out");
+  TRF_REQUIRE(src->w_ff1, "w_ff1");
+  TRF_REQUIRE(src->w_ff2, "w_ff2");
+  if (!src->b_gate || !src->b_ff1 || !src->b_ff2) return fail(TRF_ERR_ARG, "bias pointers must not be NULL");
+  hipStream_t st = as_hip(stream);
+  uint8_t* d = static_cast<uint8_t*>(dst);
+  trf::launch_pack(src->w_qkvg, trf::kQkvgRows, trf::kDim, d + trf::kOffQkvg, st);
+  trf::launch_copy_f32(src->b_gate, trf::kHeads, reinterpret_cast<float*>(d + trf::kOffBgate), st);
+  trf::launch_pack(src->w_out, trf::kDim, 512, d + trf::kOffOut, st);
+  trf::launch_pack(src->w_ff1, trf::kHidden, trf::kDim, d + trf::kOffFf1, st);
+  trf::launch_copy_f32(src->b_ff1, trf::kHidden, reinterpret_cast<float*>(d + trf::kOffBff1), st);
+  trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, d + trf::kOffFf2, st);
+  trf::launch_copy_f32(src->b_ff2, trf::kDim, reinterpret_cast<float*>(d + trf::kOffBff2), st);
+  return check_launch("pack_layer");
+}
+
+int trf_add_rmsnorm(float* X, const void* Y, int32_t y_dtype, void* out, int32_t out_dtype, int64_t n_rows,
+                    float eps, trf_stream_t stream) {
+  TRF_REQUIRE(X, "X");
+  TRF_REQUIRE(out, "out");
+  if (Y && !aligned(Y, 16)) return fail(TRF_ERR_ARG, "Y must be 16-byte aligned");
+  if ((y_dtype != TRF_F32 && y_dtype != TRF_BF16) || (out_dtype != TRF_F32 && out_dtype != TRF_BF16))
+    return fail(TRF_ERR_ARG, "dtype must be TRF_F32 or TRF_BF16");
+  if (n_rows < 0) return fail(TRF_ERR_ARG, "n_rows must be >= 0");
+  if (n_rows == 0) return TRF_OK;
+  trf::launch_add_rmsnorm(X, Y, y_dtype == TRF_BF16, out, out_dtype == TRF_BF16, n_rows, eps, as_hip(stream));
+  return check_launch("add_rmsnorm");
+}
+
+int trf_qkv_rope_gemm(const uint16_t* xn, const void* packed_layer, const float* rope, int32_t mode, int32_t batch,
+                      int32_t T, int32_t F, uint16_t* Q, uint16_t* K, uint16_t* Vt, float* G, trf_stream_t stream) {
+  if (int rc = check_mode(mode)) return rc;
+  if (int rc = check_shape(batch, T, F)) return rc;
+  TRF_REQUIRE(xn, "xn");
+  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(rope, "rope");
+  TRF_REQUIRE(Q, "Q");
+  TRF_REQUIRE(K, "K");
+  TRF_REQUIRE(Vt, "Vt");
+  TRF_REQUIRE(G, "G");
+  const trf::SeqShape sh = trf::seq_shape(mode, batch, T, F);
+  trf::launch_qkv(xn, static_cast<const uint8_t*>(packed_layer), rope, sh, Q, K, Vt, G, as_hip(stream));
+  return check_launch("qkv_rope_gemm");
+}
+
+int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G, uint16_t* O, int32_t mode,
+                  int32_t batch, int32_t T, int32_t F, trf_stream_t stream) {
+  if (int rc = check_mode(mode)) return rc;
+  if (int rc = check_shape(batch, T, F)) return rc;
+  TRF_REQUIRE(Q, "Q");
+  TRF_REQUIRE(K, "K");
+  TRF_REQUIRE(Vt, "Vt");
+  TRF_REQUIRE(G, "G");
+  TRF_REQUIRE(O, "O");
+  const trf::SeqShape sh = trf::seq_shape(mode, batch, T, F);
+  trf::launch_attention(Q, K, Vt, G, O, sh, as_hip(stream));
+  return check_launch("attention");
+}
+
+int trf_gemm_res_norm(const uint16_t* A, const void* packed_layer, int32_t which, float* X, uint16_t* xn,
+                      int64_t n_rows, float eps, trf_stream_t stream) {
+  if (which != 0 && which != 1) return fail(TRF_ERR_ARG, "which must be 0 (out-proj) or 1 (ff2), got %d", which);
+  TRF_REQUIRE(A, "A");
+  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(X, "X");
+  TRF_REQUIRE(xn, "xn");
+  if (n_rows < 0) return fail(TRF_ERR_ARG, "n_rows must be >= 0");
+  if (n_rows == 0) return TRF_OK;
+  trf::launch_gemm_res_norm(A, static_cast<const uint8_t*>(packed_layer), which, X, xn, n_rows, eps, as_hip(stream));
+  return check_launch("gemm_res_norm");
+}
+
+int trf_gemm_gelu(const uint16_t* xn, const void* packed_layer, uint16_t* H, int64_t n_rows, trf_stream_t stream) {
+  TRF_REQUIRE(xn, "xn");
+  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(H, "H");
+  if (n_rows < 0) return fail(TRF_ERR_ARG, "n_rows must be >= 0");
+  if (n_rows == 0) return TRF_OK;
+  trf::launch_gemm_gelu(xn, static_cast<const uint8_t*>(packed_layer), H, n_rows, as_hip(stream));
+  return check_launch("gemm_gelu");
+}
+
+size_t trf_stack_workspace_bytes(int32_t batch, int32_t T, int32_t F) {
+  if (check_shape(batch, T, F)) return 0;
+  return plan(batch, T, F, nullptr).bytes;
+}
+
+int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers,
+                      const int32_t* modes, int32_t n_layers, const float* rope_time, const float* rope_freq,
+                      void* workspace, size_t workspace_bytes, trf_stream_t stream) {
+  return stack_impl(X, batch, T, F, packed_layers, modes, n_layers, rope_time, rope_freq, workspace, workspace_bytes,
+                    nullptr, 0, as_hip(stream));
+}
+
+int trf_stack_forward_timed(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers,
+                            const int32_t* modes, int32_t n_layers, const float* rope_time, const float* rope_freq,
+                            void* workspace, size_t workspace_bytes, void* const* events, int32_t n_events,
+                            trf_stream_t stream) {
+  return stack_impl(X, batch, T, F, packed_layers, modes, n_layers, rope_time, rope_freq, workspace, workspace_bytes,
+                    events, n_events, as_hip(stream));
+}
+
+int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, int32_t mode,
+                   const float* rope, void* workspace, size_t workspace_bytes, trf_stream_t stream) {
+  if (int rc = check_mode(mode)) return rc;
+  if (int rc = check_shape(batch, T, F)) return rc;
+  TRF_REQUIRE(X, "X");
+  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(rope, "rope");
+  TRF_REQUIRE(workspace, "workspace");
+  const Workspace w = plan(batch, T, F, static_cast<uint8_t*>(workspace));
+  if (workspace_bytes < w.bytes)
+    return fail(TRF_ERR_WORKSPACE, "workspace is %zu bytes, need %zu", workspace_bytes, w.bytes);
+  hipStream_t st = as_hip(stream);
+  const int64_t n = int64_t(batch) * T * F;
+  trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
+  if (int rc = check_launch("add_rmsnorm")) return rc;
+  return run_attn(X, trf::seq_shape(mode, batch, T, F), static_cast<const uint8_t*>(packed_layer), rope, w, n, st);
+}
+
+int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, void* workspace,
+                 size_t workspace_bytes, trf_stream_t stream) {
+  if (int rc = check_shape(batch, T, F)) return rc;
+  TRF_REQUIRE(X, "X");
+  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(workspace, "workspace");
+  const Workspace w = plan(batch, T, F, static_cast<uint8_t*>(workspace));
+  if (workspace_bytes < w.bytes)
+    return fail(TRF_ERR_WORKSPACE, "workspace is %zu bytes, need %zu", workspace_bytes, w.bytes);
+  hipStream_t st = as_hip(stream);
+  const int64_t n = int64_t(batch) * T * F;
+  trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
+  if (int rc = check_launch("add_rmsnorm")) return rc;
+  return run_ff(X, static_cast<const uint8_t*>(packed_layer), w, n, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Internal declarations shared by the kernel and C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace trf {
+
+constexpr int kDim = 256;
+constexpr int kHeads = 8;
+constexpr int kHeadDim = 64;
+constexpr int kQkvgRows = 1544;
+constexpr int kHidden = 1024;
+
+// MFMA operand tiles: 32 output rows x 16 k per instruction, 64 lanes x 16 bytes.
+constexpr int kTileBytes = 64 * 16;
+
+// Packed sub-layer layout (byte offsets).  Every weight matrix W[rows][K] is stored as
+// tiles[rows/32][K/16][64 lanes][8 bf16] with tile[t][ks][lane][e] = W[32t + lane%32][16ks + 8(lane/32) + e]
+// (rows past the end are zero), which is the A-operand order of v_mfma_f32_32x32x16_bf16.
+constexpr int kQkvgTiles = 49;  // 1544 rows -> 49 tiles of 32 (last tile: 8 gate rows)
+constexpr size_t kOffQkvg = 0;
+constexpr size_t kSzQkvg = size_t(kQkvgTiles) * (kDim / 16) * kTileBytes;
+constexpr size_t kOffBgate = kOffQkvg + kSzQkvg;
+constexpr size_t kOffOut = kOffBgate + 256;
+constexpr size_t kSzOut = size_t(kDim / 32) * (512 / 16) * kTileBytes;
+constexpr size_t kOffFf1 = kOffOut + kSzOut;
+constexpr size_t kSzFf1 = size_t(kHidden / 32) * (kDim / 16) * kTileBytes;
+constexpr size_t kOffBff1 = kOffFf1 + kSzFf1;
+constexpr size_t kOffFf2 = kOffBff1 + kHidden * 4;
+constexpr size_t kSzFf2 = size_t(kDim / 32) * (kHidden / 16) * kTileBytes;
+constexpr size_t kOffBff2 = kOffFf2 + kSzFf2;
+constexpr size_t kLayerBytes = kOffBff2 + kDim * 4;
+
+inline int32_t seq_pad(int32_t L) { return (L + 63) / 64 * 64; }
+
+struct SeqShape {
+  int mode, batch, T, F;
+  int nseq, L, Lpad;
+};
+
+inline SeqShape seq_shape(int mode, int batch, int T, int F) {
+  SeqShape s{mode, batch, T, F, 0, 0, 0};
+  s.nseq = mode == 0 ? batch * F : batch * T;
+  s.L = mode == 0 ? T : F;
+  s.Lpad = seq_pad(s.L);
+  return s;
+}
+
+// Kernel launchers (trf_kernels.hip).  They only enqueue work; the caller checks errors.
+void launch_pack(const uint16_t* W, int rows, int K, uint8_t* dst, hipStream_t st);
+void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st);
+void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n,
+                        float eps, hipStream_t st);
+void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
+                uint16_t* Q, uint16_t* K, uint16_t* Vt, float* G, hipStream_t st);
+void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
+                      uint16_t* O, const SeqShape& sh, hipStream_t st);
+void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
+                          int64_t n, float eps, hipStream_t st);
+void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);
+
+}  // namespace trf

@@ -1,0 +1,558 @@
+// HIP kernels of the BS-RoFormer transformer stack for gfx950 (MI355X).
+//
+// All matrix products run on v_mfma_f32_32x32x16_bf16 (bf16 operands, fp32 accumulation).
+// The kernels compute C^T = W . A^T, i.e. the 32 MFMA rows are output features and the 32
+// MFMA columns are tokens.  With the 32x32 accumulator layout
+//     lane l, register r  ->  row 8*(r/4) + 4*(l/32) + (r%4), column l%32
+// every lane owns one token and runs of 4 consecutive features, so interleaved rotary pairs
+// (2p, 2p+1), row norms and residual updates need no cross-lane exchange beyond one swap of
+// the two half-waves.
+//
+// Numerics follow the reference kernels (src/turbo_roformer/csrc/kernels.cpp): fp32
+// accumulators, fp32 residual stream, fp32 rotary/softmax/gate math, bf16 round-to-nearest-even
+// for every GEMM/attention operand (kernels.cpp:30-33).
+#include "trf_internal.h"
+
+namespace trf {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.44269504088896341f;
+
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ u32x4 zero4() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+// Token index of position p in sequence s (see the token-order contract in trf_hip.h).
+__device__ __forceinline__ int64_t token_of(int mode, int s, int p, int T, int F) {
+  if (mode == 0) {
+    const int c = s / F, f = s - c * F;
+    return (int64_t(c) * T + p) * F + f;
+  }
+  return int64_t(s) * F + p;
+}
+
+// Feature offset of accumulator register group g (registers 4g..4g+3) of a 32-row tile.
+__device__ __forceinline__ int row_of_group(int g, int hh) { return 8 * g + 4 * hh; }
+
+// ============================================================ weight packing
+// dst[t][ks][lane][e] = W[32t + lane%32][16ks + 8(lane/32) + e], zero rows past `rows`.
+__global__ void k_pack(const uint16_t* __restrict__ W, int rows, int K, u32x4* __restrict__ dst) {
+  const int ksteps = K / 16;
+  const int64_t total = int64_t((rows + 31) / 32) * ksteps * 64;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int lane = int(i % 64);
+  const int ks = int((i / 64) % ksteps);
+  const int t = int(i / (64 * ksteps));
+  const int row = 32 * t + (lane & 31);
+  u32x4 v = zero4();
+  if (row < rows) v = *reinterpret_cast<const u32x4*>(W + int64_t(row) * K + 16 * ks + 8 * (lane >> 5));
+  dst[i] = v;
+}
+
+void launch_pack(const uint16_t* W, int rows, int K, uint8_t* dst, hipStream_t st) {
+  const int64_t total = int64_t((rows + 31) / 32) * (K / 16) * 64;
+  hipLaunchKernelGGL(k_pack, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, W, rows, K,
+                     reinterpret_cast<u32x4*>(dst));
+}
+
+__global__ void k_copy_f32(const float* __restrict__ src, int n, float* __restrict__ dst) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
+void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st) {
+  hipLaunchKernelGGL(k_copy_f32, dim3((n + 255) / 256), dim3(256), 0, st, src, n, dst);
+}
+
+// ============================================================ add + L2 row norm
+// One wave per row of 256: lane l holds columns 4l..4l+3.  (kernels.cpp:101-137)
+__global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ X, const void* __restrict__ Y,
+                                                     int y_bf16, void* __restrict__ out, int out_bf16,
+                                                     int64_t n, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  float* xr = X + row * kDim + 4 * lane;
+  f32x4 v = *reinterpret_cast<const f32x4*>(xr);
+  if (Y) {
+    if (y_bf16) {
+      const u32x2 y = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(Y) + row * kDim + 4 * lane);
+      v[0] += __uint_as_float(y[0] << 16);
+      v[1] += __uint_as_float(y[0] & 0xFFFF0000u);
+      v[2] += __uint_as_float(y[1] << 16);
+      v[3] += __uint_as_float(y[1] & 0xFFFF0000u);
+    } else {
+      const f32x4 y = *reinterpret_cast<const f32x4*>(static_cast<const float*>(Y) + row * kDim + 4 * lane);
+      v += y;
+    }
+    *reinterpret_cast<f32x4*>(xr) = v;
+  }
+  float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  const float inv = 1.0f / fmaxf(sqrtf(ss), eps);
+  if (out_bf16) {
+    u32x2 o = {pk_bf16(v[0] * inv, v[1] * inv), pk_bf16(v[2] * inv, v[3] * inv)};
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + row * kDim + 4 * lane) = o;
+  } else {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + row * kDim + 4 * lane) = v * inv;
+  }
+}
+
+void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n, float eps,
+                        hipStream_t st) {
+  hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, X, Y, y_bf16, out, out_bf16,
+                     n, eps);
+}
+
+// ============================================================ fused QKV + gate GEMM, rotary epilogue
+// Each wave owns 32 consecutive padded positions of one sequence and all 1544 output rows
+// (49 tiles: q heads 0-7 x 2, k x 2, v x 2, gates).  (kernels.cpp:439-540)
+__global__ __launch_bounds__(256) void k_qkv_rope(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
+                                                  const float* __restrict__ bgate, const float* __restrict__ rope,
+                                                  int mode, int nseq, int L, int Lpad, int T, int F,
+                                                  uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
+                                                  uint16_t* __restrict__ Vt, float* __restrict__ G) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hh = lane >> 5;
+  const int64_t row0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
+  if (row0 >= int64_t(nseq) * Lpad) return;
+  const int s = int(row0 / Lpad);
+  const int p = int(row0 % Lpad) + j;
+  const bool valid = p < L;
+  const int64_t tok = valid ? token_of(mode, s, p, T, F) : 0;
+
+  u32x4 bx[16];
+  {
+    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + tok * kDim);
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
+  }
+  const float* rc = rope + int64_t(valid ? p : 0) * 32;  // cos row
+  const float* rs = rc + int64_t(L) * 32;                // sin row
+
+  for (int t = 0; t < kQkvgTiles; ++t) {
+    f32x16 acc = zero16();
+    const u32x4* w = wq + int64_t(t) * 16 * 64 + lane;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) acc = mfma32(w[ks * 64], bx[ks], acc);
+
+    if (t < 32) {  // q or k: rotate interleaved pairs in fp32, store bf16 rows
+      const int h = (t & 15) >> 1;
+      uint16_t* dst = (t < 16 ? Q : K) + ((int64_t(s) * kHeads + h) * Lpad + p) * kHeadDim;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * (t & 1) + row_of_group(g, hh);
+        u32x2 o = {0u, 0u};
+        if (valid) {
+          const float c0 = rc[d0 >> 1], s0 = rs[d0 >> 1], c1 = rc[(d0 >> 1) + 1], s1 = rs[(d0 >> 1) + 1];
+          const float a0 = acc[4 * g], a1 = acc[4 * g + 1], a2 = acc[4 * g + 2], a3 = acc[4 * g + 3];
+          o[0] = pk_bf16(fmaf(a0, c0, -(a1 * s0)), fmaf(a1, c0, a0 * s0));
+          o[1] = pk_bf16(fmaf(a2, c1, -(a3 * s1)), fmaf(a3, c1, a2 * s1));
+        }
+        *reinterpret_cast<u32x2*>(dst + d0) = o;
+      }
+    } else if (t < 48) {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
+      const int h = (t - 32) >> 1;
+      uint16_t* dst = Vt + (int64_t(s) * kHeads + h) * kHeadDim * Lpad + p;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 32 * (t & 1) + row_of_group(g, hh) + r;
+          dst[int64_t(d) * Lpad] = valid ? to_bf16(acc[4 * g + r]) : uint16_t(0);
+        }
+    } else {  // gate rows 0..7 live in register group 0 of both half-waves
+      if (valid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int hd = 4 * hh + r;
+          const float z = acc[r] + bgate[hd];
+          G[tok * kHeads + hd] = 1.0f / (1.0f + expf(-z));
+        }
+      }
+    }
+  }
+}
+
+void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh, uint16_t* Q,
+                uint16_t* K, uint16_t* Vt, float* G, hipStream_t st) {
+  const int64_t rows = int64_t(sh.nseq) * sh.Lpad;
+  const unsigned blocks = unsigned((rows / 32 + 3) / 4);
+  hipLaunchKernelGGL(k_qkv_rope, dim3(blocks), dim3(256), 0, st, xn,
+                     reinterpret_cast<const u32x4*>(layer + kOffQkvg),
+                     reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.Lpad,
+                     sh.T, sh.F, Q, K, Vt, G);
+}
+
+// ============================================================ attention
+// S^T = K . Q^T puts keys on MFMA rows and queries on columns.  Key rows are loaded in the
+// order pi(i) (bits 2 and 3 of i swapped) so that register r of half-wave hh holds key
+//     key_of(r, hh) = (r < 8 ? 8*hh + r : 16 + 8*hh + (r - 8))
+// of its 32-key block: registers 0..7 / 8..15 are then exactly the 8 consecutive keys that
+// lane supplies as the B operand (P^T) of the two 16-key PV instructions O^T += V^T . P^T.
+__device__ __forceinline__ int key_perm(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+__device__ __forceinline__ int key_of(int r, int hh) { return r < 8 ? 8 * hh + r : 8 + 8 * hh + r; }
+
+// Exact softmax of one 32-query x 32-key score block held as S^T registers.
+// Returns the unnormalised bf16 probabilities as two B operands and adds the fp32 sum.
+__device__ __forceinline__ void softmax_block(const f32x16& sacc, int key0, int L, int hh, float ml, float& lsum,
+                                              u32x4& p0, u32x4& p1) {
+  float e[16];
+  if (key0 + 32 <= L) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(fmaf(sacc[r], kLog2e, -ml));
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      e[r] = (key0 + key_of(r, hh) < L) ? __builtin_amdgcn_exp2f(fmaf(sacc[r], kLog2e, -ml)) : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) lsum += e[r];
+  p0[0] = pk_bf16(e[0], e[1]);
+  p0[1] = pk_bf16(e[2], e[3]);
+  p0[2] = pk_bf16(e[4], e[5]);
+  p0[3] = pk_bf16(e[6], e[7]);
+  p1[0] = pk_bf16(e[8], e[9]);
+  p1[1] = pk_bf16(e[10], e[11]);
+  p1[2] = pk_bf16(e[12], e[13]);
+  p1[3] = pk_bf16(e[14], e[15]);
+}
+
+__device__ __forceinline__ float block_max(const f32x16& sacc, int key0, int L, int hh, float m) {
+  if (key0 + 32 <= L) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, sacc[r]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (key0 + key_of(r, hh) < L) m = fmaxf(m, sacc[r]);
+  }
+  return m;
+}
+
+// Epilogue: O[tok][h*64 + d] = bf16(acc * gate / sum), 4 consecutive features per store.
+__device__ __forceinline__ void attn_store(const f32x16 (&o)[2], int q, int L, int s, int h, int hh, int mode, int T,
+                                           int F, const float* __restrict__ G, float lsum,
+                                           uint16_t* __restrict__ O) {
+  if (q >= L) return;
+  const int64_t tok = token_of(mode, s, q, T, F);
+  const float sc = G[tok * kHeads + h] * (1.0f / lsum);
+  uint16_t* dst = O + tok * (kHeads * kHeadDim) + h * kHeadDim;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * dt + row_of_group(g, hh);
+      u32x2 v = {pk_bf16(o[dt][4 * g] * sc, o[dt][4 * g + 1] * sc),
+                 pk_bf16(o[dt][4 * g + 2] * sc, o[dt][4 * g + 3] * sc)};
+      *reinterpret_cast<u32x2*>(dst + d0) = v;
+    }
+}
+
+// Long sequences (time attention, L up to a few thousand).  One workgroup = one (sequence,
+// head) and 128 queries (4 waves x 32).  K and V^T tiles of 64 keys are staged in LDS with a
+// 16-byte-chunk XOR swizzle.  Pass 1 sweeps all keys for the exact row max; pass 2 recomputes
+// the scores, forms e = 2^(s*log2e - m*log2e), sums in fp32, rounds P to bf16 unnormalised and
+// accumulates P.V; the epilogue scales by gate/sum (kernels.cpp:286-384).
+__global__ __launch_bounds__(256) void k_attn_long(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                                                   const uint16_t* __restrict__ Vt, const float* __restrict__ G,
+                                                   uint16_t* __restrict__ O, int mode, int L, int Lpad, int T,
+                                                   int F) {
+  __shared__ u32x4 Ks[64 * 8];
+  __shared__ u32x4 Vs[64 * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, hh = lane >> 5;
+  const int sh = blockIdx.x, s = sh >> 3, h = sh & 7;
+  const uint16_t* Qh = Q + int64_t(sh) * Lpad * kHeadDim;
+  const uint16_t* Kh = K + int64_t(sh) * Lpad * kHeadDim;
+  const uint16_t* Vh = Vt + int64_t(sh) * kHeadDim * Lpad;
+  const int q = blockIdx.y * 128 + wave * 32 + j;
+
+  u32x4 qb[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    qb[ks] = q < Lpad ? reinterpret_cast<const u32x4*>(Qh + int64_t(q) * kHeadDim)[2 * ks + hh] : zero4();
+
+  const int nkt = Lpad / 64;
+  float m = -INFINITY;
+  for (int kt = 0; kt < nkt; ++kt) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i, key = c >> 3, ch = c & 7;
+      const int R = (key & 32) | key_perm(key & 31);
+      Ks[R * 8 + (ch ^ (R & 7))] = reinterpret_cast<const u32x4*>(Kh + int64_t(kt * 64 + key) * kHeadDim)[ch];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      f32x16 sacc = zero16();
+      const int R = 32 * kh + j;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(Ks[R * 8 + ((2 * ks + hh) ^ (R & 7))], qb[ks], sacc);
+      m = block_max(sacc, kt * 64 + 32 * kh, L, hh, m);
+    }
+  }
+  m = fmaxf(m, __shfl_xor(m, 32));
+  const float ml = m * kLog2e;
+
+  float lsum = 0.f;
+  f32x16 o[2] = {zero16(), zero16()};
+  for (int kt = 0; kt < nkt; ++kt) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
+      const int R = (r & 32) | key_perm(r & 31);
+      Ks[R * 8 + (ch ^ (R & 7))] = reinterpret_cast<const u32x4*>(Kh + int64_t(kt * 64 + r) * kHeadDim)[ch];
+      Vs[r * 8 + (ch ^ (r & 7))] = reinterpret_cast<const u32x4*>(Vh + int64_t(r) * Lpad + kt * 64)[ch];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      f32x16 sacc = zero16();
+      const int R = 32 * kh + j;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(Ks[R * 8 + ((2 * ks + hh) ^ (R & 7))], qb[ks], sacc);
+      u32x4 p0, p1;
+      softmax_block(sacc, kt * 64 + 32 * kh, L, hh, ml, lsum, p0, p1);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const int d = 32 * dt + j;
+        o[dt] = mfma32(Vs[d * 8 + ((4 * kh + hh) ^ (d & 7))], p0, o[dt]);
+        o[dt] = mfma32(Vs[d * 8 + ((4 * kh + 2 + hh) ^ (d & 7))], p1, o[dt]);
+      }
+    }
+  }
+  lsum += __shfl_xor(lsum, 32);
+  attn_store(o, q, L, s, h, hh, mode, T, F, G, lsum, O);
+}
+
+// Short sequences (frequency attention, L <= 64).  One wave = one (sequence, head): all
+// operands come straight from global memory into registers, the whole 64x64 score block is
+// computed once, so the exact softmax needs a single pass.
+__global__ __launch_bounds__(256) void k_attn_short(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                                                    const uint16_t* __restrict__ Vt, const float* __restrict__ G,
+                                                    uint16_t* __restrict__ O, int mode, int nsh, int L, int T,
+                                                    int F) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hh = lane >> 5;
+  const int sh = blockIdx.x * 4 + wave;
+  if (sh >= nsh) return;
+  const int s = sh >> 3, h = sh & 7;
+  constexpr int Lp = 64;
+  const uint16_t* Qh = Q + int64_t(sh) * Lp * kHeadDim;
+  const uint16_t* Kh = K + int64_t(sh) * Lp * kHeadDim;
+  const uint16_t* Vh = Vt + int64_t(sh) * kHeadDim * Lp;
+
+  u32x4 ka[2][4], va[2][4];
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      ka[kh][ks] = reinterpret_cast<const u32x4*>(Kh + int64_t(32 * kh + key_perm(j)) * kHeadDim)[2 * ks + hh];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+      va[dt][kc] = reinterpret_cast<const u32x4*>(Vh + int64_t(32 * dt + j) * Lp)[2 * kc + hh];
+
+#pragma unroll 1
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = 32 * qt + j;
+    if (32 * qt >= L) break;
+    u32x4 qb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qb[ks] = reinterpret_cast<const u32x4*>(Qh + int64_t(q) * kHeadDim)[2 * ks + hh];
+    f32x16 sacc[2];
+    float m = -INFINITY;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      sacc[kh] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sacc[kh] = mfma32(ka[kh][ks], qb[ks], sacc[kh]);
+      m = block_max(sacc[kh], 32 * kh, L, hh, m);
+    }
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const float ml = m * kLog2e;
+    float lsum = 0.f;
+    f32x16 o[2] = {zero16(), zero16()};
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      u32x4 p0, p1;
+      softmax_block(sacc[kh], 32 * kh, L, hh, ml, lsum, p0, p1);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        o[dt] = mfma32(va[dt][2 * kh], p0, o[dt]);
+        o[dt] = mfma32(va[dt][2 * kh + 1], p1, o[dt]);
+      }
+    }
+    lsum += __shfl_xor(lsum, 32);
+    attn_store(o, q, L, s, h, hh, mode, T, F, G, lsum, O);
+  }
+}
+
+void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G, uint16_t* O,
+                      const SeqShape& sh, hipStream_t st) {
+  if (sh.L <= 64) {
+    const int nsh = sh.nseq * kHeads;
+    hipLaunchKernelGGL(k_attn_short, dim3((nsh + 3) / 4), dim3(256), 0, st, Q, K, Vt, G, O, sh.mode, nsh, sh.L,
+                       sh.T, sh.F);
+  } else {
+    hipLaunchKernelGGL(k_attn_long, dim3(sh.nseq * kHeads, (sh.L + 127) / 128), dim3(256), 0, st, Q, K, Vt, G, O,
+                       sh.mode, sh.L, sh.Lpad, sh.T, sh.F);
+  }
+}
+
+// ============================================================ GEMM + residual + next norm
+// X[tok] += A[tok] . W^T (+ b); xn[tok] = X / max(|X|, eps).  Each wave owns 32 tokens and all
+// 256 output features (8 accumulator tiles), so the row norm needs one half-wave swap.
+// (kernels.cpp:542-586)
+template <int KD>
+__global__ __launch_bounds__(256) void k_gemm_res_norm(const uint16_t* __restrict__ A, const u32x4* __restrict__ wq,
+                                                       const float* __restrict__ bias, float* __restrict__ X,
+                                                       uint16_t* __restrict__ xn, int64_t n, float eps) {
+  constexpr int KS = KD / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hh = lane >> 5;
+  const int64_t tok0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
+  if (tok0 >= n) return;
+  const int64_t tok = tok0 + j;
+  const bool valid = tok < n;
+  const u32x4* ar = reinterpret_cast<const u32x4*>(A + (valid ? tok : 0) * KD);
+
+  f32x16 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = zero16();
+  for (int ks = 0; ks < KS; ++ks) {
+    const u32x4 b = valid ? ar[2 * ks + hh] : zero4();
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = mfma32(wq[(int64_t(t) * KS + ks) * 64 + lane], b, acc[t]);
+  }
+  if (!valid) return;  // no cross-lane traffic below except the half-wave swap of valid pairs
+  float* xr = X + tok * kDim;
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int f0 = 32 * t + row_of_group(g, hh);
+      f32x4 x = *reinterpret_cast<const f32x4*>(xr + f0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float y = acc[t][4 * g + r] + x[r];
+        if (bias) y += bias[f0 + r];
+        acc[t][4 * g + r] = y;
+        x[r] = y;
+        ss = fmaf(y, y, ss);
+      }
+      *reinterpret_cast<f32x4*>(xr + f0) = x;
+    }
+  ss += __shfl_xor(ss, 32);
+  const float inv = 1.0f / fmaxf(sqrtf(ss), eps);
+  uint16_t* nr = xn + tok * kDim;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int f0 = 32 * t + row_of_group(g, hh);
+      u32x2 v = {pk_bf16(acc[t][4 * g] * inv, acc[t][4 * g + 1] * inv),
+                 pk_bf16(acc[t][4 * g + 2] * inv, acc[t][4 * g + 3] * inv)};
+      *reinterpret_cast<u32x2*>(nr + f0) = v;
+    }
+}
+
+void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn, int64_t n,
+                          float eps, hipStream_t st) {
+  const unsigned blocks = unsigned((n + 127) / 128);
+  if (which == 0) {
+    hipLaunchKernelGGL(k_gemm_res_norm<512>, dim3(blocks), dim3(256), 0, st, A,
+                       reinterpret_cast<const u32x4*>(layer + kOffOut), static_cast<const float*>(nullptr), X, xn, n,
+                       eps);
+  } else {
+    hipLaunchKernelGGL(k_gemm_res_norm<1024>, dim3(blocks), dim3(256), 0, st, A,
+                       reinterpret_cast<const u32x4*>(layer + kOffFf2),
+                       reinterpret_cast<const float*>(layer + kOffBff2), X, xn, n, eps);
+  }
+}
+
+// ============================================================ FF1 GEMM + GELU
+// H = 0.5 x (1 + erf(x / sqrt 2)), x = xn . W1^T + b1  (nn.GELU() default, model.py:69).
+__global__ __launch_bounds__(256) void k_gemm_gelu(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
+                                                   const float* __restrict__ b1, uint16_t* __restrict__ H,
+                                                   int64_t n) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hh = lane >> 5;
+  const int64_t tok0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
+  if (tok0 >= n) return;
+  const int64_t tok = tok0 + j;
+  const bool valid = tok < n;
+  u32x4 bx[16];
+  {
+    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? tok : 0) * kDim);
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
+  }
+  uint16_t* hr = H + (valid ? tok : 0) * kHidden;
+  for (int t = 0; t < kHidden / 32; ++t) {
+    f32x16 acc = zero16();
+    const u32x4* w = wq + int64_t(t) * 16 * 64 + lane;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) acc = mfma32(w[ks * 64], bx[ks], acc);
+    if (valid) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int f0 = 32 * t + row_of_group(g, hh);
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = acc[4 * g + r] + b1[f0 + r];
+          v[r] = 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+        }
+        u32x2 o = {pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
+        *reinterpret_cast<u32x2*>(hr + f0) = o;
+      }
+    }
+  }
+}
+
+void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(k_gemm_gelu, dim3(unsigned((n + 127) / 128)), dim3(256), 0, st, xn,
+                     reinterpret_cast<const u32x4*>(layer + kOffFf1), reinterpret_cast<const float*>(layer + kOffBff1),
+                     H, n);
+}
+
+}  // namespace trf

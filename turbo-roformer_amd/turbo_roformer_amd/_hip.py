@@ -1,0 +1,348 @@
+"""Loader and thin torch wrappers of the gfx950 C-ABI library ``libtrf_hip.so``.
+
+Counterpart of the reference's kernel loader (src/turbo_roformer/_kernels.py): ``support()`` says
+whether the backend can run here, ``load()`` returns the library or raises ``HipUnavailable``
+(the analogue of ``KernelUnavailable``, _kernels.py:27-28), and the op wrappers below mirror the
+reference's ``torch.ops.turbo_roformer.*`` ops (kernels.cpp:644-652) on device tensors.
+
+The library is built in-tree (``make -C turbo-roformer_amd/csrc``); it shares PyTorch's HIP runtime
+(same soname), so every call is enqueued on ``torch.cuda.current_stream()``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
+HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
+ABI_VERSION = 1
+
+DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
+MODE_TIME, MODE_FREQ = 0, 1
+_F32, _BF16 = 0, 1
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class HipUnavailable(RuntimeError):
+    """The gfx950 HIP backend cannot be used here (reason in the message)."""
+
+
+class TrfLayerSrc(ctypes.Structure):
+    """``trf_layer_src`` of trf_hip.h: device pointers to one sub-layer's plain folded weights."""
+
+    _fields_ = [
+        ("w_qkvg", ctypes.c_void_p),
+        ("b_gate", ctypes.c_void_p),
+        ("w_out", ctypes.c_void_p),
+        ("w_ff1", ctypes.c_void_p),
+        ("b_ff1", ctypes.c_void_p),
+        ("w_ff2", ctypes.c_void_p),
+        ("b_ff2", ctypes.c_void_p),
+    ]
+
+
+_P, _I32, _I64, _F, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+_SIGNATURES: dict[str, tuple] = {
+    "trf_abi_version": (ctypes.c_int, []),
+    "trf_last_error": (ctypes.c_char_p, []),
+    "trf_seq_pad": (_I32, [_I32]),
+    "trf_seq_buffer_elems": (_I64, [_I32, _I32, _I32, _I32]),
+    "trf_layer_packed_bytes": (_SZ, []),
+    "trf_pack_layer": (ctypes.c_int, [ctypes.POINTER(TrfLayerSrc), _P, _P]),
+    "trf_add_rmsnorm": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I64, _F, _P]),
+    "trf_qkv_rope_gemm": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
+    "trf_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
+    "trf_gemm_res_norm": (ctypes.c_int, [_P, _P, _I32, _P, _P, _I64, _F, _P]),
+    "trf_gemm_gelu": (ctypes.c_int, [_P, _P, _P, _I64, _P]),
+    "trf_stack_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
+    "trf_stack_forward": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _P, _P, _P, _SZ, _P],
+    ),
+    "trf_stack_forward_timed": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _P, _P, _P, _SZ,
+         ctypes.POINTER(ctypes.c_void_p), _I32, _P],
+    ),
+    "trf_attn_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _P, _SZ, _P]),
+    "trf_ff_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _SZ, _P]),
+}
+
+
+def header_functions(path: Path = HEADER_PATH) -> list[str]:
+    """Names of the functions declared in trf_hip.h."""
+    text = re.sub(r"/\*.*?\*/", " ", path.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(trf_[a-z_0-9]+)\s*\(", text)))
+
+
+def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """dlopen the library and declare argument types; needs no GPU (used by the symbol checks)."""
+    if not path.exists():
+        raise HipUnavailable(f"{path.name} is not built (run `make -C turbo-roformer_amd/csrc`)")
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    if lib.trf_abi_version() != ABI_VERSION:
+        raise HipUnavailable(f"ABI version {lib.trf_abi_version()} != {ABI_VERSION}")
+    return lib
+
+
+def support() -> tuple[bool, str]:
+    """(usable, reason): library present, a ROCm GPU visible, and that GPU is a gfx950."""
+    if os.environ.get("TURBO_ROFORMER_DISABLE_HIP"):
+        return False, "disabled by TURBO_ROFORMER_DISABLE_HIP"
+    if not LIB_PATH.exists():
+        return False, f"{LIB_PATH.name} is not built"
+    if torch.version.hip is None:
+        return False, "this PyTorch has no ROCm support"
+    if not torch.cuda.is_available():
+        return False, "no ROCm GPU is visible"
+    arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+    if not arch.startswith("gfx950"):
+        return False, f"device is {arch}, the kernels are built for gfx950"
+    return True, f"gfx950 ({torch.cuda.get_device_name()})"
+
+
+def load() -> ctypes.CDLL:
+    """The library, ready to launch on the current device.  Raises HipUnavailable."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        ok, reason = support()
+        if not ok:
+            raise HipUnavailable(reason)
+        torch.cuda.init()  # the library must bind to torch's HIP runtime, loaded first
+        _lib = open_library()
+        return _lib
+
+
+def is_loaded() -> bool:
+    return _lib is not None
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = _lib.trf_last_error().decode() if _lib is not None else "unknown error"
+        raise RuntimeError(f"trf error {rc}: {msg}")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None = None) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+# ---------------------------------------------------------------------------------------------- shapes
+
+
+def seq_pad(L: int) -> int:
+    return (L + 63) // 64 * 64
+
+
+def seq_shape(mode: int, batch: int, T: int, F: int) -> tuple[int, int, int]:
+    """(number of sequences, length, padded length) of an attention mode."""
+    nseq, L = (batch * F, T) if mode == MODE_TIME else (batch * T, F)
+    return nseq, L, seq_pad(L)
+
+
+def layer_packed_bytes() -> int:
+    return int(load().trf_layer_packed_bytes())
+
+
+def workspace_bytes(batch: int, T: int, F: int) -> int:
+    n = load().trf_stack_workspace_bytes(batch, T, F)
+    if n == 0:
+        _check(1)
+    return int(n)
+
+
+# ---------------------------------------------------------------------------------------------- ops
+
+
+def pack_layer(w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2, out: torch.Tensor) -> None:
+    """Pack plain folded weights (device, row-major) into ``out`` (uint8, layer_packed_bytes())."""
+    lib = load()
+    _need(w_qkvg, "w_qkvg", torch.bfloat16, (QKVG_ROWS, DIM))
+    _need(b_gate, "b_gate", torch.float32, (HEADS,))
+    _need(w_out, "w_out", torch.bfloat16, (DIM, HEADS * HEAD_DIM))
+    _need(w_ff1, "w_ff1", torch.bfloat16, (FF_HIDDEN, DIM))
+    _need(b_ff1, "b_ff1", torch.float32, (FF_HIDDEN,))
+    _need(w_ff2, "w_ff2", torch.bfloat16, (DIM, FF_HIDDEN))
+    _need(b_ff2, "b_ff2", torch.float32, (DIM,))
+    _need(out, "out", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    src = TrfLayerSrc(*(t.data_ptr() for t in (w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2)))
+    _check(lib.trf_pack_layer(ctypes.byref(src), out.data_ptr(), _stream()))
+
+
+def add_rmsnorm(X: torch.Tensor, Y: torch.Tensor | None, out: torch.Tensor, eps: float = 1e-12) -> None:
+    """X += Y (optional); out = X / max(|X|, eps) per row (kernels.cpp:101-137)."""
+    lib = load()
+    _need(X, "X", torch.float32)
+    if X.dim() != 2 or X.shape[1] != DIM:
+        raise ValueError(f"X must be [n, {DIM}]")
+    ydt = _F32
+    if Y is not None:
+        _need(Y, "Y", Y.dtype, tuple(X.shape))
+        if Y.dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("Y must be float32 or bfloat16")
+        ydt = _BF16 if Y.dtype == torch.bfloat16 else _F32
+    _need(out, "out", out.dtype, tuple(X.shape))
+    if out.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out must be float32 or bfloat16")
+    odt = _BF16 if out.dtype == torch.bfloat16 else _F32
+    _check(lib.trf_add_rmsnorm(X.data_ptr(), _ptr(Y), ydt, out.data_ptr(), odt, X.shape[0], eps, _stream()))
+
+
+def seq_buffers(mode: int, batch: int, T: int, F: int, device="cuda") -> tuple[torch.Tensor, ...]:
+    """Q, K [nseq, 8, Lpad, 64] and Vt [nseq, 8, 64, Lpad] bf16, plus G [ntok, 8] fp32."""
+    nseq, L, Lp = seq_shape(mode, batch, T, F)
+    Q = torch.empty(nseq, HEADS, Lp, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    K = torch.empty_like(Q)
+    Vt = torch.empty(nseq, HEADS, HEAD_DIM, Lp, dtype=torch.bfloat16, device=device)
+    G = torch.empty(batch * T * F, HEADS, dtype=torch.float32, device=device)
+    return Q, K, Vt, G
+
+
+def qkv_rope_gemm(xn, layer, rope, mode, batch, T, F, Q, K, Vt, G) -> None:
+    """xn [ntok, 256] bf16 -> rotated Q, K, transposed V and sigmoid gates (kernels.cpp:439-540)."""
+    lib = load()
+    nseq, L, Lp = seq_shape(mode, batch, T, F)
+    n = batch * T * F
+    _need(xn, "xn", torch.bfloat16, (n, DIM))
+    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    _need(rope, "rope", torch.float32, (2, L, HEAD_DIM // 2))
+    _need(Q, "Q", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
+    _need(K, "K", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
+    _need(Vt, "Vt", torch.bfloat16, (nseq, HEADS, HEAD_DIM, Lp))
+    _need(G, "G", torch.float32, (n, HEADS))
+    _check(
+        lib.trf_qkv_rope_gemm(
+            xn.data_ptr(), layer.data_ptr(), rope.data_ptr(), mode, batch, T, F,
+            Q.data_ptr(), K.data_ptr(), Vt.data_ptr(), G.data_ptr(), _stream(),
+        )
+    )
+
+
+def attention(Q, K, Vt, G, O, mode, batch, T, F) -> None:
+    """Exact softmax attention + gate + head merge into O [ntok, 512] bf16 (kernels.cpp:250-388)."""
+    lib = load()
+    nseq, L, Lp = seq_shape(mode, batch, T, F)
+    n = batch * T * F
+    _need(Q, "Q", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
+    _need(K, "K", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
+    _need(Vt, "Vt", torch.bfloat16, (nseq, HEADS, HEAD_DIM, Lp))
+    _need(G, "G", torch.float32, (n, HEADS))
+    _need(O, "O", torch.bfloat16, (n, HEADS * HEAD_DIM))
+    _check(lib.trf_attention(Q.data_ptr(), K.data_ptr(), Vt.data_ptr(), G.data_ptr(), O.data_ptr(), mode, batch, T, F, _stream()))
+
+
+def gemm_res_norm(A, layer, which, X, xn, eps: float = 1e-12) -> None:
+    """X += A W^T (+b); xn = X/|X| (kernels.cpp:542-586). which 0: out-proj (K=512), 1: FF2 (K=1024)."""
+    lib = load()
+    n = X.shape[0]
+    kd = 512 if which == 0 else FF_HIDDEN
+    _need(A, "A", torch.bfloat16, (n, kd))
+    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    _need(X, "X", torch.float32, (n, DIM))
+    _need(xn, "xn", torch.bfloat16, (n, DIM))
+    _check(lib.trf_gemm_res_norm(A.data_ptr(), layer.data_ptr(), which, X.data_ptr(), xn.data_ptr(), n, eps, _stream()))
+
+
+def gemm_gelu(xn, layer, H) -> None:
+    """H = gelu_erf(xn W1^T + b1) (kernels.cpp:609-642)."""
+    lib = load()
+    n = xn.shape[0]
+    _need(xn, "xn", torch.bfloat16, (n, DIM))
+    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    _need(H, "H", torch.bfloat16, (n, FF_HIDDEN))
+    _check(lib.trf_gemm_gelu(xn.data_ptr(), layer.data_ptr(), H.data_ptr(), n, _stream()))
+
+
+SLOTS = ("qkv_rope_gemm", "attention", "gemm_out_res_norm", "gemm_ff1_gelu", "gemm_ff2_res_norm")
+
+
+def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], rope_time, rope_freq, ws,
+                  events: list | None = None) -> None:
+    """The whole stack on X [batch*T*F, 256] fp32, in place (fast.py:269-341).
+
+    ``events``: optional list of 2*5*len(layers) ``torch.cuda.Event`` (or None) recorded before/after
+    each kernel (slot order ``SLOTS``), for per-kernel timing on the launch stream."""
+    lib = load()
+    _need(X, "X", torch.float32, (batch * T * F, DIM))
+    _need(ws, "workspace", torch.uint8)
+    nb = lib.trf_layer_packed_bytes()
+    for i, t in enumerate(layers):
+        _need(t, f"layers[{i}]", torch.uint8, (nb,))
+    if len(modes) != len(layers):
+        raise ValueError("modes and layers differ in length")
+    if any(m == MODE_TIME for m in modes):
+        _need(rope_time, "rope_time", torch.float32, (2, T, HEAD_DIM // 2))
+    if any(m == MODE_FREQ for m in modes):
+        _need(rope_freq, "rope_freq", torch.float32, (2, F, HEAD_DIM // 2))
+    ptrs = (ctypes.c_void_p * max(1, len(layers)))(*[t.data_ptr() for t in layers])
+    mds = (ctypes.c_int32 * max(1, len(modes)))(*modes)
+    if events is None:
+        _check(
+            lib.trf_stack_forward(
+                X.data_ptr(), batch, T, F, ptrs, mds, len(layers), _ptr(rope_time), _ptr(rope_freq),
+                ws.data_ptr(), ws.numel(), _stream(),
+            )
+        )
+        return
+    if len(events) != 2 * len(SLOTS) * len(layers):
+        raise ValueError(f"need {2 * len(SLOTS) * len(layers)} events, got {len(events)}")
+    handles = []
+    for e in events:
+        if e is not None and not e.cuda_event:
+            e.record()  # materialise the underlying hipEvent_t
+        handles.append(None if e is None else e.cuda_event)
+    evs = (ctypes.c_void_p * len(handles))(*handles)
+    _check(
+        lib.trf_stack_forward_timed(
+            X.data_ptr(), batch, T, F, ptrs, mds, len(layers), _ptr(rope_time), _ptr(rope_freq),
+            ws.data_ptr(), ws.numel(), evs, len(handles), _stream(),
+        )
+    )
+
+
+def attn_block(X, batch, T, F, layer, mode, rope, ws) -> None:
+    """One attention sub-layer X += attn(X) on the residual stream (model.py:141)."""
+    lib = load()
+    _need(X, "X", torch.float32, (batch * T * F, DIM))
+    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    L = T if mode == MODE_TIME else F
+    _need(rope, "rope", torch.float32, (2, L, HEAD_DIM // 2))
+    _need(ws, "workspace", torch.uint8)
+    _check(lib.trf_attn_block(X.data_ptr(), batch, T, F, layer.data_ptr(), mode, rope.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
+
+
+def ff_block(X, batch, T, F, layer, ws) -> None:
+    """One feed-forward sub-layer X += ff(X) (model.py:142)."""
+    lib = load()
+    _need(X, "X", torch.float32, (batch * T * F, DIM))
+    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    _need(ws, "workspace", torch.uint8)
+    _check(lib.trf_ff_block(X.data_ptr(), batch, T, F, layer.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
