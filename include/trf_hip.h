@@ -132,7 +132,8 @@ int trf_gemm_gelu(const uint16_t* xn, const void* packed_layer, uint16_t* H, int
 size_t trf_stack_workspace_bytes(int32_t batch, int32_t T, int32_t F);
 
 /* The whole stack: one norm, then for each layer i (mode modes[i]):
- *   qkv_rope_gemm, attention, out-proj + residual + norm, FF1 + GELU, FF2 + residual + norm.
+ *   qkv_rope_gemm, attention, and one fused kernel for out-proj + residual + norm, FF1 + GELU,
+ *   FF2 + residual + norm (the FF hidden activation never reaches memory).
  * X fp32 [batch*T*F][256] is updated in place.  packed_layers is a host array of
  * n_layers device pointers (trf_pack_layer output); modes is a host array.
  * rope_time = [2][T][32], rope_freq = [2][F][32] fp32 device tables.
@@ -142,14 +143,14 @@ int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F,
                       const float* rope_time, const float* rope_freq, void* workspace,
                       size_t workspace_bytes, trf_stream_t stream);
 
-/* Kernel slots of one layer in launch order (for trf_stack_forward_timed). */
+/* Kernel slots of one layer in launch order (for trf_stack_forward_timed): the QKV GEMM, the
+ * attention, and the fused post-attention kernel (out-projection + residual + norm + FF1 + GELU +
+ * FF2 + residual + norm). */
 enum trf_kernel_slot {
   TRF_SLOT_QKV = 0,
   TRF_SLOT_ATTN = 1,
-  TRF_SLOT_OUT = 2,
-  TRF_SLOT_FF1 = 3,
-  TRF_SLOT_FF2 = 4,
-  TRF_SLOTS_PER_LAYER = 5
+  TRF_SLOT_POST = 2,
+  TRF_SLOTS_PER_LAYER = 3
 };
 
 /* trf_stack_forward that also records caller-created hipEvent_t handles around kernels:

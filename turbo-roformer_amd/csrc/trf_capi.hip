@@ -52,7 +52,6 @@ int check_mode(int32_t mode) {
 struct Workspace {
   uint16_t* xn;
   uint16_t* O;
-  uint16_t* H;
   float* G;
   uint16_t* Q;
   uint16_t* K;
@@ -80,7 +79,6 @@ Workspace plan(int32_t batch, int32_t T, int32_t F, uint8_t* base) {
   };
   w.xn = reinterpret_cast<uint16_t*>(take(n * trf::kDim * 2));
   w.O = reinterpret_cast<uint16_t*>(take(n * 512 * 2));
-  w.H = reinterpret_cast<uint16_t*>(take(n * trf::kHidden * 2));
   w.G = reinterpret_cast<float*>(take(n * trf::kHeads * 4));
   w.Q = reinterpret_cast<uint16_t*>(take(size_t(seq) * 2));
   w.K = reinterpret_cast<uint16_t*>(take(size_t(seq) * 2));
@@ -110,9 +108,10 @@ struct Events {
     if (int rc_ = (expr)) return rc_; \
   } while (0)
 
-// One attention sub-layer on an already normalised xn: qkv, attention, out-proj + residual + norm.
-int run_attn(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
-             int64_t n, hipStream_t st, const Events& ev = Events{}) {
+// One sub-layer on an already normalised xn: qkv + rotary, attention, then the fused out-proj +
+// residual + norm, and (with_ff) FF1 + GELU + FF2 + residual + norm in the same kernel.
+int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
+              int64_t n, bool with_ff, hipStream_t st, const Events& ev = Events{}) {
   TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
   trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
   TRF_TRY(check_launch("qkv_rope_gemm"));
@@ -121,22 +120,10 @@ int run_attn(float* X, const trf::SeqShape& sh, const uint8_t* layer, const floa
   trf::launch_attention(w.Q, w.K, w.Vt, w.G, w.O, sh, st);
   TRF_TRY(check_launch("attention"));
   TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
-  TRF_TRY(ev.record(TRF_SLOT_OUT, 0, st));
-  trf::launch_gemm_res_norm(w.O, layer, 0, X, w.xn, n, 1e-12f, st);
-  TRF_TRY(check_launch("gemm_res_norm(out)"));
-  return ev.record(TRF_SLOT_OUT, 1, st);
-}
-
-int run_ff(float* X, const uint8_t* layer, const Workspace& w, int64_t n, hipStream_t st,
-           const Events& ev = Events{}) {
-  TRF_TRY(ev.record(TRF_SLOT_FF1, 0, st));
-  trf::launch_gemm_gelu(w.xn, layer, w.H, n, st);
-  TRF_TRY(check_launch("gemm_gelu"));
-  TRF_TRY(ev.record(TRF_SLOT_FF1, 1, st));
-  TRF_TRY(ev.record(TRF_SLOT_FF2, 0, st));
-  trf::launch_gemm_res_norm(w.H, layer, 1, X, w.xn, n, 1e-12f, st);
-  TRF_TRY(check_launch("gemm_res_norm(ff2)"));
-  return ev.record(TRF_SLOT_FF2, 1, st);
+  TRF_TRY(ev.record(TRF_SLOT_POST, 0, st));
+  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, 1e-12f, st);
+  TRF_TRY(check_launch("post_attention"));
+  return ev.record(TRF_SLOT_POST, 1, st);
 }
 
 int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers, const int32_t* modes,
@@ -167,8 +154,7 @@ int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const*
     Events ev;
     ev.ev = n_events ? events : nullptr;
     ev.layer = i;
-    TRF_TRY(run_attn(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, st, ev));
-    TRF_TRY(run_ff(X, layer, w, n, st, ev));
+    TRF_TRY(run_layer(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, true, st, ev));
   }
   return TRF_OK;
 }
@@ -200,12 +186,12 @@ int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream) {
   if (!src->b_gate || !src->b_ff1 || !src->b_ff2) return fail(TRF_ERR_ARG, "bias pointers must not be NULL");
   hipStream_t st = as_hip(stream);
   uint8_t* d = static_cast<uint8_t*>(dst);
-  trf::launch_pack(src->w_qkvg, trf::kQkvgRows, trf::kDim, d + trf::kOffQkvg, st);
+  trf::launch_pack(src->w_qkvg, trf::kQkvgRows, trf::kDim, false, d + trf::kOffQkvg, st);
   trf::launch_copy_f32(src->b_gate, trf::kHeads, reinterpret_cast<float*>(d + trf::kOffBgate), st);
-  trf::launch_pack(src->w_out, trf::kDim, 512, d + trf::kOffOut, st);
-  trf::launch_pack(src->w_ff1, trf::kHidden, trf::kDim, d + trf::kOffFf1, st);
+  trf::launch_pack(src->w_out, trf::kDim, 512, false, d + trf::kOffOut, st);
+  trf::launch_pack(src->w_ff1, trf::kHidden, trf::kDim, true, d + trf::kOffFf1, st);
   trf::launch_copy_f32(src->b_ff1, trf::kHidden, reinterpret_cast<float*>(d + trf::kOffBff1), st);
-  trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, d + trf::kOffFf2, st);
+  trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, true, d + trf::kOffFf2, st);
   trf::launch_copy_f32(src->b_ff2, trf::kDim, reinterpret_cast<float*>(d + trf::kOffBff2), st);
   return check_launch("pack_layer");
 }
@@ -311,7 +297,8 @@ int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pa
   const int64_t n = int64_t(batch) * T * F;
   trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
   if (int rc = check_launch("add_rmsnorm")) return rc;
-  return run_attn(X, trf::seq_shape(mode, batch, T, F), static_cast<const uint8_t*>(packed_layer), rope, w, n, st);
+  return run_layer(X, trf::seq_shape(mode, batch, T, F), static_cast<const uint8_t*>(packed_layer), rope, w, n,
+                   false, st);
 }
 
 int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, void* workspace,
@@ -327,7 +314,8 @@ int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pack
   const int64_t n = int64_t(batch) * T * F;
   trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
   if (int rc = check_launch("add_rmsnorm")) return rc;
-  return run_ff(X, static_cast<const uint8_t*>(packed_layer), w, n, st);
+  trf::launch_ff(static_cast<const uint8_t*>(packed_layer), X, w.xn, n, 1e-12f, st);
+  return check_launch("feed_forward");
 }
 
 }  // extern "C"

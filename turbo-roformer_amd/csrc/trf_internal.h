@@ -16,8 +16,12 @@ constexpr int kHidden = 1024;
 constexpr int kTileBytes = 64 * 16;
 
 // Packed sub-layer layout (byte offsets).  Every weight matrix W[rows][K] is stored as
-// tiles[rows/32][K/16][64 lanes][8 bf16] with tile[t][ks][lane][e] = W[32t + lane%32][16ks + 8(lane/32) + e]
+// tiles[rows/32][K/16][64 lanes][8 bf16] with tile[t][ks][lane][e] = W[32t + lane%32][16ks + kperm(lane/32, e)]
 // (rows past the end are zero), which is the A-operand order of v_mfma_f32_32x32x16_bf16.
+// Natural order (W_qkvg, W_out): kperm(hh, e) = 8hh + e, matching B operands read as 16 contiguous
+// bytes of an activation row.  Register order (W1, W2): kperm(hh, e) = 4hh + e for e < 4 and
+// 8 + 4hh + (e - 4) otherwise, which is the order in which a 32x32 accumulator tile holds its rows in
+// a lane (runs of 4 at 8g + 4hh), so an accumulator converted to bf16 is directly the next B operand.
 constexpr int kQkvgTiles = 49;  // 1544 rows -> 49 tiles of 32 (last tile: 8 gate rows)
 constexpr size_t kOffQkvg = 0;
 constexpr size_t kSzQkvg = size_t(kQkvgTiles) * (kDim / 16) * kTileBytes;
@@ -48,7 +52,7 @@ inline SeqShape seq_shape(int mode, int batch, int T, int F) {
 }
 
 // Kernel launchers (trf_kernels.hip).  They only enqueue work; the caller checks errors.
-void launch_pack(const uint16_t* W, int rows, int K, uint8_t* dst, hipStream_t st);
+void launch_pack(const uint16_t* W, int rows, int K, bool reg_order, uint8_t* dst, hipStream_t st);
 void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st);
 void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n,
                         float eps, hipStream_t st);
@@ -59,5 +63,10 @@ void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, 
 void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
                           int64_t n, float eps, hipStream_t st);
 void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);
+// Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm].
+void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
+                      float eps, hipStream_t st);
+// Fused FF1 + GELU + FF2 + residual + norm, reading xn = X / |X| (updated in place).
+void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, float eps, hipStream_t st);
 
 }  // namespace trf

@@ -65,9 +65,14 @@ __device__ __forceinline__ int64_t token_of(int mode, int s, int p, int T, int F
 // Feature offset of accumulator register group g (registers 4g..4g+3) of a 32-row tile.
 __device__ __forceinline__ int row_of_group(int g, int hh) { return 8 * g + 4 * hh; }
 
+// Index of this wave in the workgroup, as a scalar (uniform) value so that addresses derived from it
+// stay in scalar registers.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // ============================================================ weight packing
-// dst[t][ks][lane][e] = W[32t + lane%32][16ks + 8(lane/32) + e], zero rows past `rows`.
-__global__ void k_pack(const uint16_t* __restrict__ W, int rows, int K, u32x4* __restrict__ dst) {
+// dst[t][ks][lane][e] = W[32t + lane%32][16ks + kperm(lane/32, e)], zero rows past `rows`
+// (kperm: natural 8hh + e, or register order 4hh + e / 8 + 4hh + e - 4; see trf_internal.h).
+__global__ void k_pack(const uint16_t* __restrict__ W, int rows, int K, int reg_order, u32x4* __restrict__ dst) {
   const int ksteps = K / 16;
   const int64_t total = int64_t((rows + 31) / 32) * ksteps * 64;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -76,15 +81,32 @@ __global__ void k_pack(const uint16_t* __restrict__ W, int rows, int K, u32x4* _
   const int ks = int((i / 64) % ksteps);
   const int t = int(i / (64 * ksteps));
   const int row = 32 * t + (lane & 31);
+  const int hh = lane >> 5;
   u32x4 v = zero4();
-  if (row < rows) v = *reinterpret_cast<const u32x4*>(W + int64_t(row) * K + 16 * ks + 8 * (lane >> 5));
+  if (row < rows) {
+    const uint16_t* src = W + int64_t(row) * K + 16 * ks;
+    if (reg_order) {
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(src + 4 * hh);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8 + 4 * hh);
+      v = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    } else {
+      v = *reinterpret_cast<const u32x4*>(src + 8 * hh);
+    }
+  }
   dst[i] = v;
 }
 
-void launch_pack(const uint16_t* W, int rows, int K, uint8_t* dst, hipStream_t st) {
+void launch_pack(const uint16_t* W, int rows, int K, bool reg_order, uint8_t* dst, hipStream_t st) {
   const int64_t total = int64_t((rows + 31) / 32) * (K / 16) * 64;
-  hipLaunchKernelGGL(k_pack, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, W, rows, K,
+  hipLaunchKernelGGL(k_pack, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, W, rows, K, int(reg_order),
                      reinterpret_cast<u32x4*>(dst));
+}
+
+// B operand of a k-step read from an activation row in register order (see trf_internal.h).
+__device__ __forceinline__ u32x4 load_b_regorder(const uint16_t* row, int ks, int hh) {
+  const u32x2 lo = *reinterpret_cast<const u32x2*>(row + 16 * ks + 4 * hh);
+  const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16 * ks + 8 + 4 * hh);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
 __global__ void k_copy_f32(const float* __restrict__ src, int n, float* __restrict__ dst) {
@@ -137,21 +159,81 @@ void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_
                      n, eps);
 }
 
+// ============================================================ LDS weight streaming
+// Weights are packed as 1 KB operand blocks (one MFMA A operand: 64 lanes x 16 B).  A workgroup
+// streams the blocks of one stage into LDS with direct global->LDS loads, double-buffered: while the
+// waves compute on stage s from one buffer, the blocks of stage s+1 land in the other.
+__device__ __forceinline__ void lds_load_block(const u32x4* __restrict__ src_block, u32x4* lds_block, int lane) {
+  __builtin_amdgcn_global_load_lds(src_block + lane, lds_block, 16, 0, 0);
+}
+
+// All of this thread's outstanding global loads (direct-to-LDS ones included) have landed, and every
+// wave of the workgroup has reached this point.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 // ============================================================ fused QKV + gate GEMM, rotary epilogue
-// Each wave owns 32 consecutive padded positions of one sequence and all 1544 output rows
-// (49 tiles: q heads 0-7 x 2, k x 2, v x 2, gates).  (kernels.cpp:439-540)
-__global__ __launch_bounds__(256) void k_qkv_rope(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
+// One wave owns 32 consecutive padded positions of one sequence; its 32 tokens' xn rows stay in
+// registers as B operands.  The workgroup (8 waves) streams the 49 weight tiles (q heads 0-7 x 2, k, v,
+// gates) through LDS, two tiles per stage.  (kernels.cpp:439-540)
+constexpr int kQkvWaves = 8;
+constexpr int kQkvStages = (kQkvgTiles + 1) / 2;
+
+__device__ __forceinline__ void qkv_epilogue(int t, const f32x16& acc, bool valid, int s, int p, int64_t tok, int hh,
+                                             int Lpad, const float* __restrict__ rc, const float* __restrict__ rs,
+                                             const float* __restrict__ bgate, uint16_t* __restrict__ Q,
+                                             uint16_t* __restrict__ K, uint16_t* __restrict__ Vt,
+                                             float* __restrict__ G) {
+  if (t < 32) {  // q or k: rotate interleaved pairs in fp32, store bf16 rows
+    const int h = (t & 15) >> 1;
+    uint16_t* dst = (t < 16 ? Q : K) + ((int64_t(s) * kHeads + h) * Lpad + p) * kHeadDim;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * (t & 1) + row_of_group(g, hh);
+      u32x2 o = {0u, 0u};
+      if (valid) {
+        const float c0 = rc[d0 >> 1], s0 = rs[d0 >> 1], c1 = rc[(d0 >> 1) + 1], s1 = rs[(d0 >> 1) + 1];
+        const float a0 = acc[4 * g], a1 = acc[4 * g + 1], a2 = acc[4 * g + 2], a3 = acc[4 * g + 3];
+        o[0] = pk_bf16(fmaf(a0, c0, -(a1 * s0)), fmaf(a1, c0, a0 * s0));
+        o[1] = pk_bf16(fmaf(a2, c1, -(a3 * s1)), fmaf(a3, c1, a2 * s1));
+      }
+      *reinterpret_cast<u32x2*>(dst + d0) = o;
+    }
+  } else if (t < 48) {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
+    const int h = (t - 32) >> 1;
+    uint16_t* dst = Vt + (int64_t(s) * kHeads + h) * kHeadDim * Lpad + p;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 32 * (t & 1) + row_of_group(g, hh) + r;
+        dst[int64_t(d) * Lpad] = valid ? to_bf16(acc[4 * g + r]) : uint16_t(0);
+      }
+  } else if (valid) {  // gate rows 0..7 live in register group 0 of both half-waves
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hd = 4 * hh + r;
+      const float z = acc[r] + bgate[hd];
+      G[tok * kHeads + hd] = 1.0f / (1.0f + expf(-z));
+    }
+  }
+}
+
+__global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
                                                   const float* __restrict__ bgate, const float* __restrict__ rope,
                                                   int mode, int nseq, int L, int Lpad, int T, int F,
                                                   uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
                                                   uint16_t* __restrict__ Vt, float* __restrict__ G) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ u32x4 lds[2][2 * 16 * 64];  // 2 stages x 2 tiles x 16 k-steps x 1 KB
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
-  const int64_t row0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
-  if (row0 >= int64_t(nseq) * Lpad) return;
-  const int s = int(row0 / Lpad);
-  const int p = int(row0 % Lpad) + j;
-  const bool valid = p < L;
+  const int64_t row0 = (int64_t(blockIdx.x) * kQkvWaves + wave) * 32;
+  const bool active = row0 < int64_t(nseq) * Lpad;  // inactive waves still stage weights and meet barriers
+  const int s = active ? int(row0 / Lpad) : 0;
+  const int p = active ? int(row0 % Lpad) + j : 0;
+  const bool valid = active && p < L;
   const int64_t tok = valid ? token_of(mode, s, p, T, F) : 0;
 
   u32x4 bx[16];
@@ -163,46 +245,28 @@ __global__ __launch_bounds__(256) void k_qkv_rope(const uint16_t* __restrict__ x
   const float* rc = rope + int64_t(valid ? p : 0) * 32;  // cos row
   const float* rs = rc + int64_t(L) * 32;                // sin row
 
-  for (int t = 0; t < kQkvgTiles; ++t) {
-    f32x16 acc = zero16();
-    const u32x4* w = wq + int64_t(t) * 16 * 64 + lane;
+  auto issue = [&](int stage, int buf) {
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) acc = mfma32(w[ks * 64], bx[ks], acc);
-
-    if (t < 32) {  // q or k: rotate interleaved pairs in fp32, store bf16 rows
-      const int h = (t & 15) >> 1;
-      uint16_t* dst = (t < 16 ? Q : K) + ((int64_t(s) * kHeads + h) * Lpad + p) * kHeadDim;
+    for (int i = 0; i < 4; ++i) {
+      const int b = wave * 4 + i;  // 32 blocks per stage: tile 2*stage + b/16, k-step b%16
+      const int t = 2 * stage + (b >> 4);
+      if (t < kQkvgTiles) lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, &lds[buf][b * 64], lane);
+    }
+  };
+  issue(0, 0);
+  for (int stage = 0; stage < kQkvStages; ++stage) {
+    stage_barrier();
+    if (stage + 1 < kQkvStages) issue(stage + 1, (stage + 1) & 1);
+    if (!active) continue;
+    const u32x4* Ls = lds[stage & 1];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * (t & 1) + row_of_group(g, hh);
-        u32x2 o = {0u, 0u};
-        if (valid) {
-          const float c0 = rc[d0 >> 1], s0 = rs[d0 >> 1], c1 = rc[(d0 >> 1) + 1], s1 = rs[(d0 >> 1) + 1];
-          const float a0 = acc[4 * g], a1 = acc[4 * g + 1], a2 = acc[4 * g + 2], a3 = acc[4 * g + 3];
-          o[0] = pk_bf16(fmaf(a0, c0, -(a1 * s0)), fmaf(a1, c0, a0 * s0));
-          o[1] = pk_bf16(fmaf(a2, c1, -(a3 * s1)), fmaf(a3, c1, a2 * s1));
-        }
-        *reinterpret_cast<u32x2*>(dst + d0) = o;
-      }
-    } else if (t < 48) {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
-      const int h = (t - 32) >> 1;
-      uint16_t* dst = Vt + (int64_t(s) * kHeads + h) * kHeadDim * Lpad + p;
+    for (int tt = 0; tt < 2; ++tt) {
+      const int t = 2 * stage + tt;
+      if (t >= kQkvgTiles) break;
+      f32x16 acc = zero16();
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 32 * (t & 1) + row_of_group(g, hh) + r;
-          dst[int64_t(d) * Lpad] = valid ? to_bf16(acc[4 * g + r]) : uint16_t(0);
-        }
-    } else {  // gate rows 0..7 live in register group 0 of both half-waves
-      if (valid) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int hd = 4 * hh + r;
-          const float z = acc[r] + bgate[hd];
-          G[tok * kHeads + hd] = 1.0f / (1.0f + expf(-z));
-        }
-      }
+      for (int ks = 0; ks < 16; ++ks) acc = mfma32(Ls[(tt * 16 + ks) * 64 + lane], bx[ks], acc);
+      qkv_epilogue(t, acc, valid, s, p, tok, hh, Lpad, rc, rs, bgate, Q, K, Vt, G);
     }
   }
 }
@@ -210,12 +274,13 @@ __global__ __launch_bounds__(256) void k_qkv_rope(const uint16_t* __restrict__ x
 void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh, uint16_t* Q,
                 uint16_t* K, uint16_t* Vt, float* G, hipStream_t st) {
   const int64_t rows = int64_t(sh.nseq) * sh.Lpad;
-  const unsigned blocks = unsigned((rows / 32 + 3) / 4);
-  hipLaunchKernelGGL(k_qkv_rope, dim3(blocks), dim3(256), 0, st, xn,
+  const unsigned blocks = unsigned((rows / 32 + kQkvWaves - 1) / kQkvWaves);
+  hipLaunchKernelGGL(k_qkv_rope, dim3(blocks), dim3(64 * kQkvWaves), 0, st, xn,
                      reinterpret_cast<const u32x4*>(layer + kOffQkvg),
                      reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.Lpad,
                      sh.T, sh.F, Q, K, Vt, G);
 }
+
 
 // ============================================================ attention
 // S^T = K . Q^T puts keys on MFMA rows and queries on columns.  Key rows are loaded in the
@@ -368,7 +433,7 @@ __global__ __launch_bounds__(256) void k_attn_short(const uint16_t* __restrict__
                                                     const uint16_t* __restrict__ Vt, const float* __restrict__ G,
                                                     uint16_t* __restrict__ O, int mode, int nsh, int L, int T,
                                                     int F) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int sh = blockIdx.x * 4 + wave;
   if (sh >= nsh) return;
@@ -446,7 +511,7 @@ __global__ __launch_bounds__(256) void k_gemm_res_norm(const uint16_t* __restric
                                                        const float* __restrict__ bias, float* __restrict__ X,
                                                        uint16_t* __restrict__ xn, int64_t n, float eps) {
   constexpr int KS = KD / 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int64_t tok0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
   if (tok0 >= n) return;
@@ -458,7 +523,9 @@ __global__ __launch_bounds__(256) void k_gemm_res_norm(const uint16_t* __restric
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = zero16();
   for (int ks = 0; ks < KS; ++ks) {
-    const u32x4 b = valid ? ar[2 * ks + hh] : zero4();
+    // W_out is packed in natural k order, W2 in register order (see trf_internal.h)
+    u32x4 b = zero4();
+    if (valid) b = KD == 512 ? ar[2 * ks + hh] : load_b_regorder(A + tok * KD, ks, hh);
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = mfma32(wq[(int64_t(t) * KS + ks) * 64 + lane], b, acc[t]);
   }
@@ -514,18 +581,15 @@ void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, fl
 __global__ __launch_bounds__(256) void k_gemm_gelu(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
                                                    const float* __restrict__ b1, uint16_t* __restrict__ H,
                                                    int64_t n) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int64_t tok0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
   if (tok0 >= n) return;
   const int64_t tok = tok0 + j;
   const bool valid = tok < n;
   u32x4 bx[16];
-  {
-    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? tok : 0) * kDim);
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
-  }
+  for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? load_b_regorder(xn + tok * kDim, ks, hh) : zero4();  // W1: register order
   uint16_t* hr = H + (valid ? tok : 0) * kHidden;
   for (int t = 0; t < kHidden / 32; ++t) {
     f32x16 acc = zero16();
@@ -553,6 +617,216 @@ void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int
   hipLaunchKernelGGL(k_gemm_gelu, dim3(unsigned((n + 127) / 128)), dim3(256), 0, st, xn,
                      reinterpret_cast<const u32x4*>(layer + kOffFf1), reinterpret_cast<const float*>(layer + kOffBff1),
                      H, n);
+}
+
+// ============================================================ fused post-attention block
+// out-projection + residual + norm, then FF1 + GELU + FF2 + residual + norm, for 32 tokens per wave
+// (8 waves per workgroup):
+//   acc  := X                                  (the residual stream, in the MFMA accumulators)
+//   acc  += O . Wout^T                         (8 stages of 4 k-steps)      -> X1, xn1 = X1/|X1|
+//   acc  += b2 ; for each of 32 hidden tiles:  h = xn1 . W1t^T + b1; acc += gelu(h) . W2t^T
+//   X := acc ; xn := acc / |acc|
+// xn1 and each GELU tile go from accumulator registers straight into B operands (W1, W2 are packed in
+// register order), so neither xn1 nor the 1024-wide hidden activation ever leaves the chip.
+// Replaces gemm_res_norm (out) + oneDNN FF1 + gemm_res_norm (FF2) (fast.py:311-331, kernels.cpp:542-642).
+constexpr int kMlpWaves = 8;
+constexpr int kOutStages = 8;                // 32 k-steps of W_out, 4 per stage
+constexpr int kFfStages = kHidden / 32;      // one 32-wide hidden tile per stage
+
+// erf-GELU x * Phi(x), Phi(x) = 0.5 (1 + erf(x / sqrt 2)), with erfc(|z|) from Abramowitz & Stegun
+// 7.1.26 (|error of erf| <= 1.5e-7): erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-z^2),
+// t = 1 / (1 + 0.3275911 z).  Negative x use Phi = erfc/2 directly (no cancellation).
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float p = fmaf(1.061405429f, t, -1.453152027f);
+  p = fmaf(p, t, 1.421413741f);
+  p = fmaf(p, t, -0.284496736f);
+  p = fmaf(p, t, 0.254829592f);
+  const float q = p * t * __builtin_amdgcn_exp2f(-(z * z) * kLog2e);  // erfc(|z|)
+  const float phi = x >= 0.f ? fmaf(-0.5f, q, 1.0f) : 0.5f * q;
+  return x * phi;
+}
+
+__device__ __forceinline__ float acc_inv_norm(const f32x16 (&acc)[8], float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ss = fmaf(acc[t][r], acc[t][r], ss);
+  ss += __shfl_xor(ss, 32);
+  return 1.0f / fmaxf(sqrtf(ss), eps);
+}
+
+__device__ __forceinline__ void store_row(const f32x16 (&acc)[8], float inv, float* __restrict__ xr,
+                                          uint16_t* __restrict__ nr, int hh) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int f0 = 32 * t + row_of_group(g, hh);
+      f32x4 x = {acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]};
+      *reinterpret_cast<f32x4*>(xr + f0) = x;
+      u32x2 v = {pk_bf16(x[0] * inv, x[1] * inv), pk_bf16(x[2] * inv, x[3] * inv)};
+      *reinterpret_cast<u32x2*>(nr + f0) = v;
+    }
+}
+
+template <bool OUTPROJ, bool FF>
+__global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, const uint8_t* __restrict__ layer,
+                                             float* __restrict__ X, uint16_t* __restrict__ xn, int64_t n, float eps) {
+  __shared__ u32x4 lds[2][32 * 64];  // 2 stages x 32 operand blocks of 1 KB
+  const u32x4* wo = reinterpret_cast<const u32x4*>(layer + kOffOut);
+  const u32x4* w1 = reinterpret_cast<const u32x4*>(layer + kOffFf1);
+  const u32x4* w2 = reinterpret_cast<const u32x4*>(layer + kOffFf2);
+  const float* b1 = reinterpret_cast<const float*>(layer + kOffBff1);
+  const float* b2 = reinterpret_cast<const float*>(layer + kOffBff2);
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int j = lane & 31, hh = lane >> 5;
+  const int64_t tok = (int64_t(blockIdx.x) * kMlpWaves + wave) * 32 + j;
+  // Lanes past the last token work on a copy of the last token's row (every MFMA column and the
+  // half-wave norm swap stay within one token) and store nothing.
+  const bool valid = tok < n;
+  const int64_t trow = valid ? tok : n - 1;
+  float* xr = X + trow * kDim;
+  uint16_t* nr = xn + trow * kDim;
+
+  f32x16 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(xr + 32 * t + row_of_group(g, hh));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][4 * g + r] = x[r];
+    }
+
+  u32x4 xb[16];  // FF1 B operands (xn in register order)
+  auto add_b2 = [&]() {  // a few bias vectors at a time: the accumulators already fill most registers
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 32 * t + row_of_group(g, hh));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][4 * g + r] += b[r];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if (!OUTPROJ) {
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) xb[ks] = load_b_regorder(nr, ks, hh);
+    add_b2();
+  }
+
+  constexpr int s_begin = OUTPROJ ? 0 : kOutStages;
+  constexpr int s_end = FF ? kOutStages + kFfStages : kOutStages;  // stages: W_out k-steps, then hidden tiles
+  auto issue = [&](int s, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = wave * 4 + i;  // 32 blocks per stage
+      const u32x4* src;
+      if (s < kOutStages) {
+        src = wo + (int64_t(b >> 2) * 32 + 4 * s + (b & 3)) * 64;  // W_out tile b/4, k-step 4s + b%4
+      } else {
+        const int ht = s - kOutStages;
+        src = b < 16 ? w1 + (int64_t(ht) * 16 + b) * 64                             // W1 tile ht, k-step b
+                     : w2 + (int64_t((b - 16) >> 1) * 64 + 2 * ht + (b & 1)) * 64;  // W2 tile (b-16)/2, k-step 2ht + b%2
+      }
+      lds_load_block(src, &lds[buf][b * 64], lane);
+    }
+  };
+
+  const uint16_t* orow = O + trow * 512;
+  u32x4 ob[4];
+  auto load_o = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ob[i] = reinterpret_cast<const u32x4*>(orow)[2 * (4 * s + i) + hh];
+  };
+  if (OUTPROJ) load_o(0);
+  issue(s_begin, 0);
+
+  if (OUTPROJ) {
+    for (int s = 0; s < kOutStages; ++s) {
+      stage_barrier();
+      if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
+      const u32x4* Ls = lds[s & 1];
+      u32x4 cur[4] = {ob[0], ob[1], ob[2], ob[3]};
+      if (s + 1 < kOutStages) load_o(s + 1);
+#pragma unroll
+      for (int ksl = 0; ksl < 4; ++ksl) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = mfma32(Ls[(t * 4 + ksl) * 64 + lane], cur[ksl], acc[t]);
+        __builtin_amdgcn_sched_barrier(0);  // bound the LDS operands in flight (register budget)
+      }
+    }
+    const float inv = acc_inv_norm(acc, eps);
+    if (!FF) {
+      if (valid) store_row(acc, inv, xr, nr, hh);
+      return;
+    }
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const int t = ks >> 1, g0 = 2 * (ks & 1);
+      xb[ks] = u32x4{pk_bf16(acc[t][4 * g0] * inv, acc[t][4 * g0 + 1] * inv),
+                     pk_bf16(acc[t][4 * g0 + 2] * inv, acc[t][4 * g0 + 3] * inv),
+                     pk_bf16(acc[t][4 * g0 + 4] * inv, acc[t][4 * g0 + 5] * inv),
+                     pk_bf16(acc[t][4 * g0 + 6] * inv, acc[t][4 * g0 + 7] * inv)};
+    }
+    add_b2();
+  }
+  if (FF) {
+    for (int s = kOutStages; s < s_end; ++s) {
+      stage_barrier();
+      if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
+      const u32x4* Ls = lds[s & 1];
+      const int ht = s - kOutStages;
+      f32x16 h = zero16();
+#pragma unroll
+      for (int kg = 0; kg < 4; ++kg) {
+#pragma unroll
+        for (int ks = 4 * kg; ks < 4 * kg + 4; ++ks) h = mfma32(Ls[ks * 64 + lane], xb[ks], h);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      u32x4 hb[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float v[8];
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(b1 + 32 * ht + row_of_group(2 * c + gg, hh));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[4 * gg + r] = gelu_erf(h[8 * c + 4 * gg + r] + bb[r]);
+        }
+        hb[c] = u32x4{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]), pk_bf16(v[6], v[7])};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ot = 0; ot < 8; ++ot) {
+        acc[ot] = mfma32(Ls[(16 + 2 * ot) * 64 + lane], hb[0], acc[ot]);
+        acc[ot] = mfma32(Ls[(17 + 2 * ot) * 64 + lane], hb[1], acc[ot]);
+        if (ot & 1) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    const float inv = acc_inv_norm(acc, eps);
+    if (valid) store_row(acc, inv, xr, nr, hh);
+  }
+}
+
+void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
+                      float eps, hipStream_t st) {
+  const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
+  if (with_ff)
+    hipLaunchKernelGGL((k_mlp<true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+  else
+    hipLaunchKernelGGL((k_mlp<true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+}
+
+void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, float eps, hipStream_t st) {
+  const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
+  hipLaunchKernelGGL((k_mlp<false, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st,
+                     static_cast<const uint16_t*>(nullptr), layer, X, xn, n, eps);
 }
 
 }  // namespace trf

@@ -281,7 +281,7 @@ def gemm_gelu(xn, layer, H) -> None:
     _check(lib.trf_gemm_gelu(xn.data_ptr(), layer.data_ptr(), H.data_ptr(), n, _stream()))
 
 
-SLOTS = ("qkv_rope_gemm", "attention", "gemm_out_res_norm", "gemm_ff1_gelu", "gemm_ff2_res_norm")
+SLOTS = ("qkv_rope_gemm", "attention", "post_attention")  # trf_kernel_slot order
 
 
 def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], rope_time, rope_freq, ws,
