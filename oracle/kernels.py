@@ -45,7 +45,11 @@ def add_rmsnorm(X: Tensor, Y: Tensor | None, out_dtype=torch.bfloat16) -> tuple[
 
 def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, batch: int, T: int, F: int):
     """qkv_rope_gemm (kernels.cpp:439-540): fp32 accumulators, fp32 rotary of q and k, bf16 outputs,
-    fp32 sigmoid gates.  Returns Q, K, Vt (padded, zero pads) and G."""
+    fp32 sigmoid gates.  Returns Q, K, Vt (padded, zero pads) and G.
+
+    Device contract: q leaves multiplied by log2(e) (in fp32, before its single bf16 rounding), so that
+    q.k is the base-2 exponent of the softmax; the reference multiplies by log2(e) inside its exp
+    (kernels.cpp:333-339).  The two differ only in where q is rounded."""
     n = xn.shape[0]
     acc = (xn.double() @ W.double().t()).float()  # [n, 1544]
     g = torch.sigmoid(acc[:, 3 * H * DH :].double() + b_gate.double()).float()
@@ -58,7 +62,7 @@ def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, ba
         x = acc[:, part * H * DH : (part + 1) * H * DH].view(n, H, DH)
         return x[idx].permute(0, 2, 1, 3)
 
-    q = reference.rotate(seq(0), ang).to(torch.bfloat16)
+    q = (reference.rotate(seq(0), ang) * torch.tensor(LOG2E, dtype=torch.float32)).to(torch.bfloat16)
     k = reference.rotate(seq(1), ang).to(torch.bfloat16)
     v = seq(2).to(torch.bfloat16)
     Q = torch.zeros(nseq, H, Lp, DH, dtype=torch.bfloat16)
@@ -72,8 +76,9 @@ def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, ba
 
 def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int, T: int, F: int,
               chunk: int = 64) -> Tensor:
-    """attention (kernels.cpp:250-388): exact row max over valid keys, e = 2^(s log2e - m log2e) in fp32,
-    unnormalised bf16 P, fp32 row sum of e, O = (P V) * gate / sum rounded to bf16, token order."""
+    """attention (kernels.cpp:250-388): exact row max over valid keys, e = 2^(s - m) in fp32 (Q carries
+    log2(e), see qkv_rope), unnormalised bf16 P, fp32 row sum of e, O = (P V) * gate / sum rounded to
+    bf16, token order."""
     idx = token_index(mode, batch, T, F)
     nseq, L = idx.shape
     O = torch.empty(batch * T * F, H * DH, dtype=torch.bfloat16)
@@ -84,7 +89,7 @@ def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int
         v = Vt[s0:s1, :, :, :L].double().transpose(-1, -2)
         S = (q @ k.transpose(-1, -2)).float()
         m = S.amax(dim=-1, keepdim=True)
-        e = torch.exp2(S * LOG2E - m * LOG2E)  # fp32
+        e = torch.exp2(S - m)  # fp32
         rs = e.double().sum(dim=-1, keepdim=True)
         o = e.to(torch.bfloat16).double() @ v  # [s, H, L, DH]
         tok = idx[s0:s1]  # [s, L]

@@ -8,6 +8,8 @@ flip allowed in 1e-4 of the elements) and a per-op SNR floor.
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -115,12 +117,13 @@ def test_attention(hip, layers, mode, batch, T, F):
     _hip.attention(Q.to(DEV), K.to(DEV), Vt.to(DEV), G.to(DEV), O, mode, batch, T, F)
     torch.cuda.synchronize()
     assert_bf16_close(Oref, O, "O", min_snr=48)
-    # against textbook fp64 softmax attention on the same bf16 operands (no bf16 P): SNR only
+    # against textbook fp64 softmax attention on the same bf16 operands (no bf16 P): SNR only.
+    # Q carries log2(e), so the natural-log scores are q.k * ln 2.
     L = T if mode == 0 else F
     idx = ok.token_index(mode, batch, T, F)
     q, k = Q[:, :, :L].double(), K[:, :, :L].double()
     v = Vt[:, :, :, :L].double().transpose(-1, -2)
-    o = torch.softmax(q @ k.transpose(-1, -2), dim=-1) @ v
+    o = torch.softmax((q @ k.transpose(-1, -2)) * math.log(2.0), dim=-1) @ v
     o = o * G[idx].permute(0, 2, 1).unsqueeze(-1).double()
     exact = torch.empty(n, 8, 64, dtype=torch.float64)
     exact[idx] = o.permute(0, 2, 1, 3)

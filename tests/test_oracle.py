@@ -137,7 +137,8 @@ def test_emulated_attention_rows_and_gate():
         Vt[:, :, j, j] = 1.0
     G = torch.rand(5, 8, generator=g)
     O = ok.attention(Q, K, Vt, G, 0, batch, T, F_).float().view(5, 8, 64)
-    p = torch.softmax(Q[0, :, :5].double() @ K[0, :, :5].double().transpose(-1, -2), -1)  # [8, 5, 5]
+    # Q carries log2(e): the natural-log scores are q.k * ln 2
+    p = torch.softmax(Q[0, :, :5].double() @ K[0, :, :5].double().transpose(-1, -2) * math.log(2.0), -1)
     torch.testing.assert_close(O[:, :, :5], (p * G.t().double()[:, :, None]).permute(1, 0, 2).float(), rtol=1e-2, atol=2e-3)
     torch.testing.assert_close(O.sum(-1), G, rtol=2e-2, atol=0)
     assert (O[:, :, 5:] == 0).all()

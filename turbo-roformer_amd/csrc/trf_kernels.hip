@@ -41,10 +41,9 @@ __device__ __forceinline__ uint16_t to_bf16(float x) {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
 
+// A zero splat: as the first accumulator of an MFMA chain it folds into the inline constant 0.
 __device__ __forceinline__ f32x16 zero16() {
-  f32x16 z;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  f32x16 z = {};
   return z;
 }
 
@@ -196,8 +195,10 @@ __device__ __forceinline__ void qkv_epilogue(int t, const f32x16& acc, bool vali
       if (valid) {
         const float c0 = rc[d0 >> 1], s0 = rs[d0 >> 1], c1 = rc[(d0 >> 1) + 1], s1 = rs[(d0 >> 1) + 1];
         const float a0 = acc[4 * g], a1 = acc[4 * g + 1], a2 = acc[4 * g + 2], a3 = acc[4 * g + 3];
-        o[0] = pk_bf16(fmaf(a0, c0, -(a1 * s0)), fmaf(a1, c0, a0 * s0));
-        o[1] = pk_bf16(fmaf(a2, c1, -(a3 * s1)), fmaf(a3, c1, a2 * s1));
+        // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
+        const float sc = t < 16 ? kLog2e : 1.0f;
+        o[0] = pk_bf16(fmaf(a0, c0, -(a1 * s0)) * sc, fmaf(a1, c0, a0 * s0) * sc);
+        o[1] = pk_bf16(fmaf(a2, c1, -(a3 * s1)) * sc, fmaf(a3, c1, a2 * s1) * sc);
       }
       *reinterpret_cast<u32x2*>(dst + d0) = o;
     }
@@ -293,16 +294,18 @@ __device__ __forceinline__ int key_of(int r, int hh) { return r < 8 ? 8 * hh + r
 
 // Exact softmax of one 32-query x 32-key score block held as S^T registers.
 // Returns the unnormalised bf16 probabilities as two B operands and adds the fp32 sum.
-__device__ __forceinline__ void softmax_block(const f32x16& sacc, int key0, int L, int hh, float ml, float& lsum,
+// Scores are in units of log2(e) (q is pre-scaled), so e = 2^(s - m); with shift = 0 the caller has
+// already subtracted the row max inside the MFMA accumulator.
+__device__ __forceinline__ void softmax_block(const f32x16& sacc, int key0, int L, int hh, float shift, float& lsum,
                                               u32x4& p0, u32x4& p1) {
   float e[16];
   if (key0 + 32 <= L) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(fmaf(sacc[r], kLog2e, -ml));
+    for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(sacc[r] - shift);
   } else {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      e[r] = (key0 + key_of(r, hh) < L) ? __builtin_amdgcn_exp2f(fmaf(sacc[r], kLog2e, -ml)) : 0.f;
+      e[r] = (key0 + key_of(r, hh) < L) ? __builtin_amdgcn_exp2f(sacc[r] - shift) : 0.f;
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) lsum += e[r];
@@ -319,7 +322,7 @@ __device__ __forceinline__ void softmax_block(const f32x16& sacc, int key0, int 
 __device__ __forceinline__ float block_max(const f32x16& sacc, int key0, int L, int hh, float m) {
   if (key0 + 32 <= L) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) m = fmaxf(m, sacc[r]);
+    for (int r = 0; r < 16; r += 2) m = fmaxf(m, fmaxf(sacc[r], sacc[r + 1]));  // v_max3_f32
   } else {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
@@ -347,83 +350,174 @@ __device__ __forceinline__ void attn_store(const f32x16 (&o)[2], int q, int L, i
     }
 }
 
-// Long sequences (time attention, L up to a few thousand).  One workgroup = one (sequence,
-// head) and 128 queries (4 waves x 32).  K and V^T tiles of 64 keys are staged in LDS with a
-// 16-byte-chunk XOR swizzle.  Pass 1 sweeps all keys for the exact row max; pass 2 recomputes
-// the scores, forms e = 2^(s*log2e - m*log2e), sums in fp32, rounds P to bf16 unnormalised and
-// accumulates P.V; the epilogue scales by gate/sum (kernels.cpp:286-384).
-__global__ __launch_bounds__(256) void k_attn_long(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                                                   const uint16_t* __restrict__ Vt, const float* __restrict__ G,
-                                                   uint16_t* __restrict__ O, int mode, int L, int Lpad, int T,
-                                                   int F) {
-  __shared__ u32x4 Ks[64 * 8];
-  __shared__ u32x4 Vs[64 * 8];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int j = lane & 31, hh = lane >> 5;
-  const int sh = blockIdx.x, s = sh >> 3, h = sh & 7;
-  const uint16_t* Qh = Q + int64_t(sh) * Lpad * kHeadDim;
-  const uint16_t* Kh = K + int64_t(sh) * Lpad * kHeadDim;
-  const uint16_t* Vh = Vt + int64_t(sh) * kHeadDim * Lpad;
-  const int q = blockIdx.y * 128 + wave * 32 + j;
+// Long sequences (time attention, L up to a few thousand).  Exact, non-online softmax in two passes
+// (kernels.cpp:286-384): pass 1 sweeps all keys for the row max m; pass 2 recomputes the scores, forms
+// e = 2^(s - m) (q carries the factor log2(e), so scores are base-2 exponents), sums e in fp32, rounds
+// P = e to bf16 unnormalised and accumulates P.V; the epilogue scales by gate/sum.
+// One workgroup = one (sequence, head) and 4 waves x 64 queries; each wave holds two 32-query column
+// tiles, so every K or V^T operand read from LDS feeds two MFMAs.  Tiles of 64 keys of K and V^T are
+// double-buffered in LDS, loaded global->LDS directly, with the XOR swizzle of the 16-byte chunks
+// (bank-conflict-free operand reads) applied through each lane's source address.  Only the last key
+// tile can hold keys >= L, so the masked code runs once per pass.
+constexpr int kAttWaves = 4;
+constexpr int kAttQT = 2;                       // 32-query column tiles per wave
+constexpr int kAttBlockQ = kAttWaves * 32 * kAttQT;  // queries per workgroup
 
-  u32x4 qb[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qb[ks] = q < Lpad ? reinterpret_cast<const u32x4*>(Qh + int64_t(q) * kHeadDim)[2 * ks + hh] : zero4();
+// Physical 16-byte chunk of logical chunk c in LDS row R is c ^ chunk_swz(R).  Operand reads touch
+// rows R0..R0+31 at one logical chunk; with 64 four-byte banks (two 128-byte rows per bank sweep) this
+// pattern is conflict-free for every group of 16 lanes (and for groups of 8 with 32 banks).
+__device__ __forceinline__ int chunk_swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
 
-  const int nkt = Lpad / 64;
-  float m = -INFINITY;
-  for (int kt = 0; kt < nkt; ++kt) {
-    __syncthreads();
+// This wave's share of staging one 8 KB tile (64 rows x 8 chunks of 16 B) into LDS: rows 16w..16w+15
+// (two instructions of 8 rows).  Row R of the K tile holds key (R&32)|pi(R&31); row R of the V^T tile
+// holds head feature R.
+__device__ __forceinline__ void stage_k_tile(const uint16_t* __restrict__ Kh, int kt, u32x4* lds_tile, int wave,
+                                             int lane) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i, key = c >> 3, ch = c & 7;
-      const int R = (key & 32) | key_perm(key & 31);
-      Ks[R * 8 + (ch ^ (R & 7))] = reinterpret_cast<const u32x4*>(Kh + int64_t(kt * 64 + key) * kHeadDim)[ch];
-    }
-    __syncthreads();
+  for (int i = 0; i < 2; ++i) {
+    const int R = 16 * wave + 8 * i + (lane >> 3), pc = lane & 7;
+    const int key = (R & 32) | key_perm(R & 31);
+    const uint16_t* src = Kh + int64_t(kt * 64 + key) * kHeadDim + 8 * (pc ^ chunk_swz(R));
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src), lds_tile + (16 * wave + 8 * i) * 8, 16,
+                                     0, 0);
+  }
+}
+
+__device__ __forceinline__ void stage_v_tile(const uint16_t* __restrict__ Vh, int kt, int Lpad, u32x4* lds_tile,
+                                             int wave, int lane) {
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
+  for (int i = 0; i < 2; ++i) {
+    const int R = 16 * wave + 8 * i + (lane >> 3), pc = lane & 7;
+    const uint16_t* src = Vh + int64_t(R) * Lpad + kt * 64 + 8 * (pc ^ chunk_swz(R));
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src), lds_tile + (16 * wave + 8 * i) * 8, 16,
+                                     0, 0);
+  }
+}
+
+// K operands of one 32-key half of a tile.
+__device__ __forceinline__ void load_k_half(const u32x4* __restrict__ Kl, int kh, int j, int hh, u32x4 (&ka)[4]) {
+  const int R = 32 * kh + j;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ka[ks] = Kl[R * 8 + ((2 * ks + hh) ^ chunk_swz(R))];
+}
+
+// Pass-1 work of one 64-key tile: scores for both query tiles, running max.
+template <bool MASK>
+__device__ __forceinline__ void attn_max_tile(const u32x4* __restrict__ Kl, const u32x4 (&qb)[kAttQT][4], int key0,
+                                              int L, int j, int hh, float (&m)[kAttQT]) {
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh) {
+    u32x4 ka[4];
+    load_k_half(Kl, kh, j, hh, ka);
+#pragma unroll
+    for (int qt = 0; qt < kAttQT; ++qt) {
       f32x16 sacc = zero16();
-      const int R = 32 * kh + j;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(Ks[R * 8 + ((2 * ks + hh) ^ (R & 7))], qb[ks], sacc);
-      m = block_max(sacc, kt * 64 + 32 * kh, L, hh, m);
+      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[qt][ks], sacc);
+      m[qt] = MASK ? block_max(sacc, key0 + 32 * kh, L, hh, m[qt]) : block_max(sacc, 0, 32, hh, m[qt]);
     }
   }
-  m = fmaxf(m, __shfl_xor(m, 32));
-  const float ml = m * kLog2e;
+}
 
-  float lsum = 0.f;
-  f32x16 o[2] = {zero16(), zero16()};
-  for (int kt = 0; kt < nkt; ++kt) {
-    __syncthreads();
+// Pass-2 work of one 64-key tile: scores, exact-softmax probabilities, P.V accumulation.
+template <bool MASK>
+__device__ __forceinline__ void attn_pv_tile(const u32x4* __restrict__ Kl, const u32x4* __restrict__ Vl,
+                                             const u32x4 (&qb)[kAttQT][4], int key0, int L, int j, int hh,
+                                             const float (&m)[kAttQT], float (&lsum)[kAttQT],
+                                             f32x16 (&o)[kAttQT][2]) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
-      const int R = (r & 32) | key_perm(r & 31);
-      Ks[R * 8 + (ch ^ (R & 7))] = reinterpret_cast<const u32x4*>(Kh + int64_t(kt * 64 + r) * kHeadDim)[ch];
-      Vs[r * 8 + (ch ^ (r & 7))] = reinterpret_cast<const u32x4*>(Vh + int64_t(r) * Lpad + kt * 64)[ch];
-    }
-    __syncthreads();
+  for (int kh = 0; kh < 2; ++kh) {
+    u32x4 ka[4];
+    load_k_half(Kl, kh, j, hh, ka);
+    u32x4 p0[kAttQT], p1[kAttQT];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
+    for (int qt = 0; qt < kAttQT; ++qt) {
       f32x16 sacc = zero16();
-      const int R = 32 * kh + j;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(Ks[R * 8 + ((2 * ks + hh) ^ (R & 7))], qb[ks], sacc);
-      u32x4 p0, p1;
-      softmax_block(sacc, kt * 64 + 32 * kh, L, hh, ml, lsum, p0, p1);
+      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[qt][ks], sacc);
+      softmax_block(sacc, MASK ? key0 + 32 * kh : 0, MASK ? L : 32, hh, m[qt], lsum[qt], p0[qt], p1[qt]);
+    }
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const int d = 32 * dt + j;
-        o[dt] = mfma32(Vs[d * 8 + ((4 * kh + hh) ^ (d & 7))], p0, o[dt]);
-        o[dt] = mfma32(Vs[d * 8 + ((4 * kh + 2 + hh) ^ (d & 7))], p1, o[dt]);
+    for (int dt = 0; dt < 2; ++dt) {
+      const int d = 32 * dt + j;
+      const u32x4 v0 = Vl[d * 8 + ((4 * kh + hh) ^ chunk_swz(d))];
+      const u32x4 v1 = Vl[d * 8 + ((4 * kh + 2 + hh) ^ chunk_swz(d))];
+#pragma unroll
+      for (int qt = 0; qt < kAttQT; ++qt) {
+        o[qt][dt] = mfma32(v0, p0[qt], o[qt][dt]);
+        o[qt][dt] = mfma32(v1, p1[qt], o[qt][dt]);
       }
     }
   }
-  lsum += __shfl_xor(lsum, 32);
-  attn_store(o, q, L, s, h, hh, mode, T, F, G, lsum, O);
+}
+
+__global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                                                   const uint16_t* __restrict__ Vt, const float* __restrict__ G,
+                                                   uint16_t* __restrict__ O, int mode, int L, int Lpad, int T,
+                                                   int F, int nqb) {
+  __shared__ u32x4 lds[2][2][64 * 8];  // [buffer][K, V^T][64 rows x 8 chunks]
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int j = lane & 31, hh = lane >> 5;
+  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs (8 L2 caches), so block b runs on
+  // XCD b % 8.  Give all query blocks of one (sequence, head) consecutive slots of one XCD, so its K and
+  // V^T are fetched from HBM once into that XCD's L2 (nseq * 8 heads is a multiple of 8).
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;  // grid = nseq * 8 * nqb blocks
+  const int sh = xcd + 8 * (slot / nqb), qblk = slot % nqb;
+  const int s = sh >> 3, h = sh & 7;
+  const uint16_t* Qh = Q + int64_t(sh) * Lpad * kHeadDim;
+  const uint16_t* Kh = K + int64_t(sh) * Lpad * kHeadDim;
+  const uint16_t* Vh = Vt + int64_t(sh) * kHeadDim * Lpad;
+  const int q0 = qblk * kAttBlockQ + wave * 32 * kAttQT;
+  const bool active = q0 < L;  // idle waves still stage tiles and meet every barrier
+
+  u32x4 qb[kAttQT][4];
+#pragma unroll
+  for (int qt = 0; qt < kAttQT; ++qt) {
+    const int q = q0 + 32 * qt + j;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qb[qt][ks] = q < Lpad ? reinterpret_cast<const u32x4*>(Qh + int64_t(q) * kHeadDim)[2 * ks + hh] : zero4();
+  }
+
+  const int nkt = Lpad / 64;
+  // ---- pass 1: exact row max over all valid keys
+  float m[kAttQT];
+#pragma unroll
+  for (int qt = 0; qt < kAttQT; ++qt) m[qt] = -INFINITY;
+  stage_k_tile(Kh, 0, lds[0][0], wave, lane);
+  for (int kt = 0; kt < nkt - 1; ++kt) {
+    stage_barrier();
+    stage_k_tile(Kh, kt + 1, lds[(kt + 1) & 1][0], wave, lane);
+    if (active) attn_max_tile<false>(lds[kt & 1][0], qb, 0, L, j, hh, m);
+  }
+  stage_barrier();
+  if (active) attn_max_tile<true>(lds[(nkt - 1) & 1][0], qb, (nkt - 1) * 64, L, j, hh, m);
+  float lsum[kAttQT];
+#pragma unroll
+  for (int qt = 0; qt < kAttQT; ++qt) {
+    m[qt] = fmaxf(m[qt], __shfl_xor(m[qt], 32));
+    lsum[qt] = 0.f;
+  }
+
+  // ---- pass 2: probabilities and P.V
+  f32x16 o[kAttQT][2];
+#pragma unroll
+  for (int qt = 0; qt < kAttQT; ++qt) o[qt][0] = o[qt][1] = zero16();
+  stage_barrier();  // everyone is done with the pass-1 buffers before they are overwritten
+  stage_k_tile(Kh, 0, lds[0][0], wave, lane);
+  stage_v_tile(Vh, 0, Lpad, lds[0][1], wave, lane);
+  for (int kt = 0; kt < nkt - 1; ++kt) {
+    stage_barrier();
+    stage_k_tile(Kh, kt + 1, lds[(kt + 1) & 1][0], wave, lane);
+    stage_v_tile(Vh, kt + 1, Lpad, lds[(kt + 1) & 1][1], wave, lane);
+    if (active) attn_pv_tile<false>(lds[kt & 1][0], lds[kt & 1][1], qb, 0, L, j, hh, m, lsum, o);
+  }
+  stage_barrier();
+  if (!active) return;
+  attn_pv_tile<true>(lds[(nkt - 1) & 1][0], lds[(nkt - 1) & 1][1], qb, (nkt - 1) * 64, L, j, hh, m, lsum, o);
+#pragma unroll
+  for (int qt = 0; qt < kAttQT; ++qt)
+    attn_store(o[qt], q0 + 32 * qt + j, L, s, h, hh, mode, T, F, G, lsum[qt] + __shfl_xor(lsum[qt], 32), O);
 }
 
 // Short sequences (frequency attention, L <= 64).  One wave = one (sequence, head): all
@@ -472,7 +566,7 @@ __global__ __launch_bounds__(256) void k_attn_short(const uint16_t* __restrict__
       m = block_max(sacc[kh], 32 * kh, L, hh, m);
     }
     m = fmaxf(m, __shfl_xor(m, 32));
-    const float ml = m * kLog2e;
+    const float ml = m;  // scores are already in units of log2(e)
     float lsum = 0.f;
     f32x16 o[2] = {zero16(), zero16()};
 #pragma unroll
@@ -497,8 +591,9 @@ void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, 
     hipLaunchKernelGGL(k_attn_short, dim3((nsh + 3) / 4), dim3(256), 0, st, Q, K, Vt, G, O, sh.mode, nsh, sh.L,
                        sh.T, sh.F);
   } else {
-    hipLaunchKernelGGL(k_attn_long, dim3(sh.nseq * kHeads, (sh.L + 127) / 128), dim3(256), 0, st, Q, K, Vt, G, O,
-                       sh.mode, sh.L, sh.Lpad, sh.T, sh.F);
+    const int nqb = (sh.L + kAttBlockQ - 1) / kAttBlockQ;
+    hipLaunchKernelGGL(k_attn_long, dim3(sh.nseq * kHeads * nqb), dim3(64 * kAttWaves), 0, st, Q, K, Vt, G, O,
+                       sh.mode, sh.L, sh.Lpad, sh.T, sh.F, nqb);
   }
 }
 
