@@ -18,7 +18,7 @@
  *
  * Sequence buffers (written by trf_qkv_rope_gemm, read by trf_attention), bf16, with
  * Lpad = trf_seq_pad(L) and sequence s, head h, position p, head feature d:
- *     Q  [nseq][8][Lpad][64]   index ((s*8 + h)*Lpad + p)*64 + d   (rotated, scale folded)
+ *     Q  [nseq][8][Lpad][64]   index ((s*8 + h)*Lpad + p)*64 + d   (rotated, times log2(e))
  *     K  [nseq][8][Lpad][64]   same index                         (rotated)
  *     Vt [nseq][8][64][Lpad]   index ((s*8 + h)*64 + d)*Lpad + p   (transposed V)
  * Positions p >= L are written as zeros.  G is fp32 [ntok][8] = sigmoid(gate logits).
@@ -102,13 +102,17 @@ int trf_add_rmsnorm(float* X, const void* Y, int32_t y_dtype, void* out, int32_t
 
 /* xn [ntok][256] bf16 -> Q, K, Vt (layouts above) and G = sigmoid(xn.Wg + b_gate).
  * Rotary on q, k in fp32 from the accumulators with the caller's fp32 tables
- * rope = [2][L][32] (cos then sin, angle = p * 10000^(-2i/64)).
+ * rope = [2][L][32] (cos then sin, angle = p * 10000^(-2i/64)).  The 1/8 attention scale is
+ * folded into the q rows of the weights; q is further multiplied by log2(e) in fp32 before its
+ * single bf16 rounding, so trf_attention's scores are base-2 exponents.
  * Replaces qkv_rope_gemm (kernels.cpp:439-540). */
 int trf_qkv_rope_gemm(const uint16_t* xn, const void* packed_layer, const float* rope, int32_t mode,
                       int32_t batch, int32_t T, int32_t F, uint16_t* Q, uint16_t* K, uint16_t* Vt,
                       float* G, trf_stream_t stream);
 
-/* Exact (two-pass, non-online) softmax attention per (sequence, head); epilogue
+/* Exact (two-pass, non-online) softmax attention per (sequence, head): with s = q.k (q as
+ * written by trf_qkv_rope_gemm), m = max over keys, P = bf16(2^(s - m)) unnormalised and the
+ * row sum in fp32, the epilogue writes
  * O[tok][h*64 + d] = gate[tok][h] / rowsum * (P V)[.][d] in token order, bf16.
  * Replaces attention (kernels.cpp:250-388). */
 int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
