@@ -35,9 +35,25 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
+TRAFFIC_SUMMARY = ROOT / "profiles" / "attention_time_17s_chunk_hbm_traffic.md"
+COPY_CALIBRATION_BYTES = 1 << 30  # one plain 1 GiB device copy: 1 GiB read + 1 GiB written
+
+
 def attn_flops(nseq: int, L: int) -> float:
     """Algorithmic FLOPs of one attention call: QK^T and PV, 2*L*L*64 each, per (sequence, head)."""
     return 4.0 * nseq * 8 * L * L * 64
+
+
+def measured_traffic() -> float | None:
+    """HBM bytes per time-attention launch from the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary
+    (each pass already scaled by the same counter's reading for a plain copy of known size), or None."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch ="):
+                return float(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def tune_malloc() -> None:
@@ -70,6 +86,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and mask-SNR leg")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one plain 1 GiB device copy, the known-size reference for HBM counters")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the stack runs on a single MI355X (no multi-GPU path is built)",
@@ -91,6 +109,13 @@ def main() -> int:
     X = torch.empty_like(Xd0)
     nl = len(stack.layers)
     nslot = len(_hip.SLOTS)
+
+    if a.copy_calibration:
+        src = torch.ones(COPY_CALIBRATION_BYTES // 4, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(a.warmup):
         X.copy_(Xd0)
@@ -149,7 +174,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "flops_per_launch": flops_t,
             "avg_launch_ms": round(attn_t_ms, 4),
         },
