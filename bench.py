@@ -86,6 +86,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and mask-SNR leg")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--precision", choices=("ff_split", "bf16"), default="ff_split",
+                    help="FF GEMM arithmetic: split-bf16 operands (default) or all-bf16 as the reference kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one plain 1 GiB device copy, the known-size reference for HBM counters")
     a = ap.parse_args()
@@ -104,11 +106,7 @@ def main() -> int:
     raw = torch.from_numpy(signals.noise_mix(SAMPLES, seed=a.seed))[None]
     X0 = host.band_split(host.spectrogram(raw))  # (1, T, F, 256) fp32
     _, T, F, _ = X0.shape
-    stack = HipStack(sd, "cuda")
     Xd0 = X0.reshape(-1, 256).contiguous().cuda()
-    X = torch.empty_like(Xd0)
-    nl = len(stack.layers)
-    nslot = len(_hip.SLOTS)
 
     if a.copy_calibration:
         src = torch.ones(COPY_CALIBRATION_BYTES // 4, device="cuda")
@@ -117,38 +115,51 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    for _ in range(a.warmup):
-        X.copy_(Xd0)
-        stack(X, 1, T, F)
-    torch.cuda.synchronize()
+    def timed(precision: str, with_events: bool):
+        """(ms per stack forward, per-kernel ms or None, output) for one precision."""
+        stack = HipStack(sd, "cuda", precision=precision)
+        X = torch.empty_like(Xd0)
+        nslot = len(_hip.SLOTS)
+        for _ in range(a.warmup):
+            X.copy_(Xd0)
+            stack(X, 1, T, F)
+        torch.cuda.synchronize()
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nslot * len(stack.layers))]
+                  for _ in range(a.steps)] if with_events else [None] * a.steps
+        for evs in events:  # create the underlying events outside the timed region
+            for e in evs or ():
+                e.record()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(a.steps):
+            X.copy_(Xd0)
+            stack(X, 1, T, F, events=events[k])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ms = (t1 - t0) * 1e3 / a.steps
+        print(f"bench: {a.steps} timed stack forwards ({precision}), {ms:.3f} ms each", file=sys.stderr, flush=True)
+        kernel_ms = None
+        if with_events:
+            per_kernel: dict[str, list[float]] = {}
+            for evs in events:
+                for i, mode in enumerate(stack.modes):
+                    for sl, name in enumerate(_hip.SLOTS):
+                        key = f"{name}_{'t' if mode == 0 else 'f'}"
+                        dt = evs[2 * (i * nslot + sl)].elapsed_time(evs[2 * (i * nslot + sl) + 1])
+                        per_kernel.setdefault(key, []).append(dt)
+            kernel_ms = {k: float(np.mean(v)) for k, v in per_kernel.items()}
+        out = X.view(1, T, F, 256).cpu()
+        del stack, X
+        torch.cuda.empty_cache()
+        return ms, kernel_ms, out
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nslot * nl)] for _ in range(a.steps)]
-    for evs in events:  # create the underlying events outside the timed region
-        for e in evs:
-            e.record()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(a.steps):
-        X.copy_(Xd0)
-        stack(X, 1, T, F, events=events[k])
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / a.steps
-    print(f"bench: {a.steps} timed stack forwards, {ms:.3f} ms each", file=sys.stderr, flush=True)
-
-    per_kernel: dict[str, list[float]] = {}
-    for evs in events:
-        for i, mode in enumerate(stack.modes):
-            for s, name in enumerate(_hip.SLOTS):
-                key = f"{name}_{'t' if mode == 0 else 'f'}"
-                dt = evs[2 * (i * nslot + s)].elapsed_time(evs[2 * (i * nslot + s) + 1])
-                per_kernel.setdefault(key, []).append(dt)
-    kernel_ms = {k: float(np.mean(v)) for k, v in per_kernel.items()}
+    ms, kernel_ms, out_gpu = timed(a.precision, True)
+    alt = "bf16" if a.precision == "ff_split" else "ff_split"
+    ms_alt, _, out_alt = timed(alt, False)
     attn_t_ms = kernel_ms["attention_t"]
     flops_t = attn_flops(F, T)
     achieved = flops_t / (attn_t_ms * 1e-3) / 1e12
 
-    out_gpu = X.view(1, T, F, 256).cpu()
     result = {
         "metric": "17s-chunk stack forwards/sec; time-attn TFLOP/s and % of bf16 MFMA peak",
         "value": round(1e3 / ms, 3),
@@ -179,6 +190,8 @@ def main() -> int:
             "avg_launch_ms": round(attn_t_ms, 4),
         },
         "kernels_ms_per_launch": {k: round(v, 4) for k, v in sorted(kernel_ms.items())},
+        "precision": a.precision,
+        "other_precision": {"precision": alt, "ms_per_step": round(ms_alt, 4), "value": round(1e3 / ms_alt, 3)},
     }
 
     if not a.no_cpu:
@@ -196,6 +209,8 @@ def main() -> int:
         m_ref = reference.mask_from_stack(ref, sd, cfg)
         m_gpu = reference.mask_from_stack(out_gpu, sd, cfg)
         snr_mask = signals.snr_db(m_ref.numpy(), m_gpu.numpy())
+        m_alt = reference.mask_from_stack(out_alt, sd, cfg)
+        snr_mask_alt = signals.snr_db(m_ref.numpy(), m_alt.numpy())
         result["cpu_baseline"] = {
             "value": round(1.0 / cpu_s, 5),
             "unit": "stack forwards/s",
@@ -206,7 +221,8 @@ def main() -> int:
                       f"{'avx512_bf16' in cpu_flags()}",
             "gpu_speedup": round((1e3 / ms) * cpu_s, 1),
         }
-        result["parity"] = {"mask_snr_db_vs_fp32": round(snr_mask, 2), "stack_out_snr_db_vs_fp32": round(snr_x, 2)}
+        result["parity"] = {"mask_snr_db_vs_fp32": round(snr_mask, 2), "stack_out_snr_db_vs_fp32": round(snr_x, 2),
+                            f"mask_snr_db_vs_fp32_{alt}": round(snr_mask_alt, 2)}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 1
+#define TRF_ABI_VERSION 2
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -55,6 +55,16 @@ enum trf_mode { TRF_MODE_TIME = 0, TRF_MODE_FREQ = 1 };
 
 enum trf_dtype { TRF_F32 = 0, TRF_BF16 = 1 };
 
+/* Arithmetic of the feed-forward GEMMs.
+ * TRF_PREC_BF16: every GEMM operand is rounded to bf16, as the reference kernels do
+ *   (kernels.cpp:30-33, docs/how-it-works.md:164-170).
+ * TRF_PREC_FF_SPLIT: FF1 and FF2 take split-bf16 operands v = hi + lo (hi = bf16(v),
+ *   lo = bf16(v - hi)) and compute hi.hi + hi.lo + lo.hi on the bf16 MFMA with fp32
+ *   accumulation, which removes the four rounding points (W1, W2, xn, gelu(h)) that dominate the
+ *   bf16 design's error.  It needs the lo weight parts (trf_layer_src.w_ff1_lo / w_ff2_lo).
+ *   Attention, the QKV GEMM and the out-projection stay bf16 in both modes. */
+enum trf_precision { TRF_PREC_BF16 = 0, TRF_PREC_FF_SPLIT = 1 };
+
 /* Same type as hipStream_t; NULL is the default stream. */
 typedef struct ihipStream_t* trf_stream_t;
 
@@ -71,6 +81,10 @@ typedef struct trf_layer_src {
   const float* b_ff1;     /* fp32 [1024] */
   const uint16_t* w_ff2;  /* bf16 [256][1024] */
   const float* b_ff2;     /* fp32 [256] */
+  /* Optional (NULL = zero): bf16 residuals w - bf16(w) of the fp32 folded W1 and W2, used by
+   * TRF_PREC_FF_SPLIT.  Same shapes as w_ff1 / w_ff2. */
+  const uint16_t* w_ff1_lo;
+  const uint16_t* w_ff2_lo;
 } trf_layer_src;
 
 /* ---------------------------------------------------------------- library */
@@ -140,12 +154,13 @@ size_t trf_stack_workspace_bytes(int32_t batch, int32_t T, int32_t F);
  *   FF2 + residual + norm (the FF hidden activation never reaches memory).
  * X fp32 [batch*T*F][256] is updated in place.  packed_layers is a host array of
  * n_layers device pointers (trf_pack_layer output); modes is a host array.
+ * precision is a trf_precision value for the feed-forward GEMMs.
  * rope_time = [2][T][32], rope_freq = [2][F][32] fp32 device tables.
  * Replaces FastBSRoformer._transformer_cpp (fast.py:269-341). */
 int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F,
                       const void* const* packed_layers, const int32_t* modes, int32_t n_layers,
-                      const float* rope_time, const float* rope_freq, void* workspace,
-                      size_t workspace_bytes, trf_stream_t stream);
+                      int32_t precision, const float* rope_time, const float* rope_freq,
+                      void* workspace, size_t workspace_bytes, trf_stream_t stream);
 
 /* Kernel slots of one layer in launch order (for trf_stack_forward_timed): the QKV GEMM, the
  * attention, and the fused post-attention kernel (out-projection + residual + norm + FF1 + GELU +
@@ -163,7 +178,8 @@ enum trf_kernel_slot {
  * counterpart of the reference's per-section wall-clock profile (fast.py:62-80, 279-340). */
 int trf_stack_forward_timed(float* X, int32_t batch, int32_t T, int32_t F,
                             const void* const* packed_layers, const int32_t* modes,
-                            int32_t n_layers, const float* rope_time, const float* rope_freq,
+                            int32_t n_layers, int32_t precision, const float* rope_time,
+                            const float* rope_freq,
                             void* workspace, size_t workspace_bytes, void* const* events,
                             int32_t n_events, trf_stream_t stream);
 
@@ -175,9 +191,9 @@ int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pa
                    trf_stream_t stream);
 
 /* One feed-forward sub-layer: X += W2 gelu(W1 norm(X) + b1) + b2 ("x = ff(x) + x",
- * model.py:142). */
+ * model.py:142), with the FF GEMMs in the given trf_precision. */
 int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer,
-                 void* workspace, size_t workspace_bytes, trf_stream_t stream);
+                 int32_t precision, void* workspace, size_t workspace_bytes, trf_stream_t stream);
 
 #ifdef __cplusplus
 }

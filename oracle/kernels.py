@@ -114,6 +114,32 @@ def gemm_gelu(xn: Tensor, W1: Tensor, b1: Tensor) -> Tensor:
     return (0.5 * x.double() * (1.0 + torch.erf(x.double() / math.sqrt(2.0)))).to(torch.bfloat16)
 
 
+def split_bf16(x: Tensor) -> tuple[Tensor, Tensor]:
+    """Split-bf16 parts of fp32 x: hi = bf16(x), lo = bf16(x - hi)."""
+    x = x.float()
+    hi = x.to(torch.bfloat16)
+    return hi, (x - hi.float()).to(torch.bfloat16)
+
+
+def split_matmul(a: Tensor, w_hi: Tensor, w_lo: Tensor) -> Tensor:
+    """a W^T from split-bf16 operands: hi.hi + lo.hi + hi.lo (the lo.lo term dropped), fp64 sums, fp32 out."""
+    ah, al = split_bf16(a)
+    wh, wl = w_hi.double().t(), w_lo.double().t()
+    return (ah.double() @ wh + al.double() @ wh + ah.double() @ wl).float()
+
+
+def ff_split(X: Tensor, W1: Tensor, b1: Tensor, W2: Tensor, b2: Tensor) -> tuple[Tensor, Tensor]:
+    """The feed-forward sub-layer in the library's split precision (TRF_PREC_FF_SPLIT): xn = X/|X| in
+    fp32, both GEMMs on split-bf16 operands of xn, W1, gelu(h), W2 (fp32 weights split here); returns the
+    fp32 residual stream and the bf16 xn of the result.  Not a reference kernel: this is the library's
+    own higher-precision mode, checked against the fp32 forward."""
+    xn = (X.double() / X.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).float()
+    h = split_matmul(xn, *split_bf16(W1)) + b1.float()
+    g = (0.5 * h.double() * (1.0 + torch.erf(h.double() / math.sqrt(2.0)))).float()
+    y = X.float() + split_matmul(g, *split_bf16(W2)) + b2.float()
+    return y, (y.double() / y.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).to(torch.bfloat16)
+
+
 def bf16_weights(P: dict) -> dict:
     """bf16 operands of one folded sub-layer (oracle.folded.fold output), as the kernels see them."""
     return dict(
@@ -124,9 +150,10 @@ def bf16_weights(P: dict) -> dict:
 
 
 @torch.no_grad()
-def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int) -> Tensor:
+def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int, precision: str = "bf16") -> Tensor:
     """The fused-op sequence of ``_transformer_cpp`` (fast.py:269-341) with bf16 rounding at the same
-    points as the reference kernels; X is [batch*T*F, 256] fp32, returns a new tensor."""
+    points as the reference kernels; X is [batch*T*F, 256] fp32, returns a new tensor.
+    ``precision="ff_split"`` replaces the feed-forward by ``ff_split``."""
     X = X.float().clone()
     _, xn = add_rmsnorm(X, None)
     for P in layers:
@@ -134,6 +161,9 @@ def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int) -> Tensor:
         Q, K, Vt, G = qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], w["mode"], batch, T, F)
         O = attention(Q, K, Vt, G, w["mode"], batch, T, F)
         X, xn = gemm_res_norm(O, w["Wo"], None, X)
+        if precision == "ff_split":
+            X, xn = ff_split(X, P["W1"], P["b1"], P["W2"], P["b2"])
+            continue
         Hh = gemm_gelu(xn, w["W1"], w["b1"])
         X, xn = gemm_res_norm(Hh, w["W2"], w["b2"], X)
     return X

@@ -157,3 +157,34 @@ def test_kernel_emulation_pads_and_layouts():
     v = (xn[tok].double() @ W[1024:1536].double().t()).float().to(torch.bfloat16).view(8, 64)
     assert torch.equal(Vt[5, :, :, 5], v)
     np.testing.assert_allclose(G[tok].numpy(), torch.sigmoid(xn[tok].double() @ W[1536:].double().t()).numpy(), rtol=1e-6)
+
+
+def test_split_bf16_parts_and_products():
+    """hi is the bf16 rounding, hi + lo recovers x to 2^-16 relative, and the three-product matmul is
+    ~2^-16-accurate where the plain bf16 product is ~2^-8 (a dropped or transposed term fails this)."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(64, 256, generator=g)
+    hi, lo = ok.split_bf16(x)
+    assert torch.equal(hi, x.to(torch.bfloat16))
+    assert ((hi.double() + lo.double() - x.double()).abs() <= x.double().abs() * 2.0**-16).all()
+    w = 0.05 * torch.randn(96, 256, generator=g)
+    exact = x.double() @ w.double().t()
+    err_split = (ok.split_matmul(x, *ok.split_bf16(w)).double() - exact).norm() / exact.norm()
+    err_bf16 = (x.to(torch.bfloat16).double() @ w.to(torch.bfloat16).double().t() - exact).norm() / exact.norm()
+    assert err_split < 2e-5 < 1e-3 < err_bf16
+    # every term matters: without lo.hi or hi.lo the error is bf16-sized again
+    wh, wl = ok.split_bf16(w)
+    no_lo_hi = (hi.double() @ wh.double().t() + hi.double() @ wl.double().t() - exact).norm() / exact.norm()
+    assert no_lo_hi > 1e-3
+
+
+def test_ff_split_matches_fp32_feed_forward(tiny_sd):
+    """The split-precision FF sub-layer equals the fp32 FF of the reference module to ~1e-5."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(300, 256, generator=g)
+    prefix = "layers.0.0.layers.0.1"
+    ref = reference.feed_forward(x.double(), {k: v.double() for k, v in tiny_sd.items()}, prefix) + x.double()
+    P = folded.fold(tiny_sd, CFG["depth"])[0]
+    y, xn = ok.ff_split(x, P["W1"], P["b1"], P["W2"], P["b2"])
+    assert snr_db(ref.numpy(), y.double().numpy()) >= 90.0
+    assert torch.equal(xn, (y.double() / y.double().norm(dim=-1, keepdim=True)).to(torch.bfloat16))

@@ -38,6 +38,12 @@ int check_shape(int32_t batch, int32_t T, int32_t F) {
   return TRF_OK;
 }
 
+int check_precision(int32_t precision) {
+  if (precision != TRF_PREC_BF16 && precision != TRF_PREC_FF_SPLIT)
+    return fail(TRF_ERR_ARG, "precision must be 0 (bf16) or 1 (ff split), got %d", precision);
+  return TRF_OK;
+}
+
 int check_mode(int32_t mode) {
   if (mode != TRF_MODE_TIME && mode != TRF_MODE_FREQ) return fail(TRF_ERR_ARG, "mode must be 0 (time) or 1 (freq), got %d", mode);
   return TRF_OK;
@@ -111,7 +117,7 @@ struct Events {
 // One sub-layer on an already normalised xn: qkv + rotary, attention, then the fused out-proj +
 // residual + norm, and (with_ff) FF1 + GELU + FF2 + residual + norm in the same kernel.
 int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
-              int64_t n, bool with_ff, hipStream_t st, const Events& ev = Events{}) {
+              int64_t n, bool with_ff, bool split_ff, hipStream_t st, const Events& ev = Events{}) {
   TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
   trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
   TRF_TRY(check_launch("qkv_rope_gemm"));
@@ -121,15 +127,16 @@ int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const flo
   TRF_TRY(check_launch("attention"));
   TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
   TRF_TRY(ev.record(TRF_SLOT_POST, 0, st));
-  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, 1e-12f, st);
+  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, split_ff, 1e-12f, st);
   TRF_TRY(check_launch("post_attention"));
   return ev.record(TRF_SLOT_POST, 1, st);
 }
 
 int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers, const int32_t* modes,
-               int32_t n_layers, const float* rope_time, const float* rope_freq, void* workspace,
-               size_t workspace_bytes, void* const* events, int32_t n_events, hipStream_t st) {
+               int32_t n_layers, int32_t precision, const float* rope_time, const float* rope_freq,
+               void* workspace, size_t workspace_bytes, void* const* events, int32_t n_events, hipStream_t st) {
   TRF_TRY(check_shape(batch, T, F));
+  TRF_TRY(check_precision(precision));
   TRF_REQUIRE(X, "X");
   TRF_REQUIRE(workspace, "workspace");
   if (n_layers < 0) return fail(TRF_ERR_ARG, "n_layers must be >= 0");
@@ -154,7 +161,8 @@ int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const*
     Events ev;
     ev.ev = n_events ? events : nullptr;
     ev.layer = i;
-    TRF_TRY(run_layer(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, true, st, ev));
+    TRF_TRY(run_layer(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, true,
+                      precision == TRF_PREC_FF_SPLIT, st, ev));
   }
   return TRF_OK;
 }
@@ -183,6 +191,8 @@ int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream) {
   TRF_REQUIRE(src->w_out, "w_out");
   TRF_REQUIRE(src->w_ff1, "w_ff1");
   TRF_REQUIRE(src->w_ff2, "w_ff2");
+  if ((src->w_ff1_lo && !aligned(src->w_ff1_lo, 16)) || (src->w_ff2_lo && !aligned(src->w_ff2_lo, 16)))
+    return fail(TRF_ERR_ARG, "w_ff1_lo and w_ff2_lo must be 16-byte aligned");
   if (!src->b_gate || !src->b_ff1 || !src->b_ff2) return fail(TRF_ERR_ARG, "bias pointers must not be NULL");
   hipStream_t st = as_hip(stream);
   uint8_t* d = static_cast<uint8_t*>(dst);
@@ -193,6 +203,16 @@ int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream) {
   trf::launch_copy_f32(src->b_ff1, trf::kHidden, reinterpret_cast<float*>(d + trf::kOffBff1), st);
   trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, true, d + trf::kOffFf2, st);
   trf::launch_copy_f32(src->b_ff2, trf::kDim, reinterpret_cast<float*>(d + trf::kOffBff2), st);
+  if (src->w_ff1_lo) {
+    trf::launch_pack(src->w_ff1_lo, trf::kHidden, trf::kDim, true, d + trf::kOffFf1Lo, st);
+  } else if (hipMemsetAsync(d + trf::kOffFf1Lo, 0, trf::kSzFf1, st) != hipSuccess) {
+    return check_launch("pack_layer (w_ff1_lo)");
+  }
+  if (src->w_ff2_lo) {
+    trf::launch_pack(src->w_ff2_lo, trf::kDim, trf::kHidden, true, d + trf::kOffFf2Lo, st);
+  } else if (hipMemsetAsync(d + trf::kOffFf2Lo, 0, trf::kSzFf2, st) != hipSuccess) {
+    return check_launch("pack_layer (w_ff2_lo)");
+  }
   return check_launch("pack_layer");
 }
 
@@ -268,18 +288,18 @@ size_t trf_stack_workspace_bytes(int32_t batch, int32_t T, int32_t F) {
 }
 
 int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers,
-                      const int32_t* modes, int32_t n_layers, const float* rope_time, const float* rope_freq,
-                      void* workspace, size_t workspace_bytes, trf_stream_t stream) {
-  return stack_impl(X, batch, T, F, packed_layers, modes, n_layers, rope_time, rope_freq, workspace, workspace_bytes,
-                    nullptr, 0, as_hip(stream));
+                      const int32_t* modes, int32_t n_layers, int32_t precision, const float* rope_time,
+                      const float* rope_freq, void* workspace, size_t workspace_bytes, trf_stream_t stream) {
+  return stack_impl(X, batch, T, F, packed_layers, modes, n_layers, precision, rope_time, rope_freq, workspace,
+                    workspace_bytes, nullptr, 0, as_hip(stream));
 }
 
 int trf_stack_forward_timed(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers,
-                            const int32_t* modes, int32_t n_layers, const float* rope_time, const float* rope_freq,
-                            void* workspace, size_t workspace_bytes, void* const* events, int32_t n_events,
-                            trf_stream_t stream) {
-  return stack_impl(X, batch, T, F, packed_layers, modes, n_layers, rope_time, rope_freq, workspace, workspace_bytes,
-                    events, n_events, as_hip(stream));
+                            const int32_t* modes, int32_t n_layers, int32_t precision, const float* rope_time,
+                            const float* rope_freq, void* workspace, size_t workspace_bytes, void* const* events,
+                            int32_t n_events, trf_stream_t stream) {
+  return stack_impl(X, batch, T, F, packed_layers, modes, n_layers, precision, rope_time, rope_freq, workspace,
+                    workspace_bytes, events, n_events, as_hip(stream));
 }
 
 int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, int32_t mode,
@@ -298,12 +318,13 @@ int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pa
   trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
   if (int rc = check_launch("add_rmsnorm")) return rc;
   return run_layer(X, trf::seq_shape(mode, batch, T, F), static_cast<const uint8_t*>(packed_layer), rope, w, n,
-                   false, st);
+                   false, false, st);
 }
 
-int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, void* workspace,
-                 size_t workspace_bytes, trf_stream_t stream) {
+int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, int32_t precision,
+                 void* workspace, size_t workspace_bytes, trf_stream_t stream) {
   if (int rc = check_shape(batch, T, F)) return rc;
+  if (int rc = check_precision(precision)) return rc;
   TRF_REQUIRE(X, "X");
   TRF_REQUIRE(packed_layer, "packed_layer");
   TRF_REQUIRE(workspace, "workspace");
@@ -314,7 +335,7 @@ int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pack
   const int64_t n = int64_t(batch) * T * F;
   trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
   if (int rc = check_launch("add_rmsnorm")) return rc;
-  trf::launch_ff(static_cast<const uint8_t*>(packed_layer), X, w.xn, n, 1e-12f, st);
+  trf::launch_ff(static_cast<const uint8_t*>(packed_layer), X, w.xn, n, precision == TRF_PREC_FF_SPLIT, 1e-12f, st);
   return check_launch("feed_forward");
 }
 

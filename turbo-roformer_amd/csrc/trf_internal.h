@@ -34,7 +34,10 @@ constexpr size_t kOffBff1 = kOffFf1 + kSzFf1;
 constexpr size_t kOffFf2 = kOffBff1 + kHidden * 4;
 constexpr size_t kSzFf2 = size_t(kDim / 32) * (kHidden / 16) * kTileBytes;
 constexpr size_t kOffBff2 = kOffFf2 + kSzFf2;
-constexpr size_t kLayerBytes = kOffBff2 + kDim * 4;
+// Low parts of W1 and W2 (bf16(W - bf16(W))), same tiling, for the split-bf16 feed-forward.
+constexpr size_t kOffFf1Lo = kOffBff2 + kDim * 4;
+constexpr size_t kOffFf2Lo = kOffFf1Lo + kSzFf1;
+constexpr size_t kLayerBytes = kOffFf2Lo + kSzFf2;
 
 inline int32_t seq_pad(int32_t L) { return (L + 63) / 64 * 64; }
 
@@ -63,10 +66,12 @@ void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, 
 void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
                           int64_t n, float eps, hipStream_t st);
 void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);
-// Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm].
+// Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm].  split_ff selects
+// split-bf16 operands (hi + lo) for both FF GEMMs.
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
-                      float eps, hipStream_t st);
-// Fused FF1 + GELU + FF2 + residual + norm, reading xn = X / |X| (updated in place).
-void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, float eps, hipStream_t st);
+                      bool split_ff, float eps, hipStream_t st);
+// Fused FF1 + GELU + FF2 + residual + norm on X (updated in place); xn is written as X / |X|.
+// The bf16 variant reads its FF1 input from xn, the split variant normalises X itself.
+void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool split_ff, float eps, hipStream_t st);
 
 }  // namespace trf

@@ -909,8 +909,195 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
   }
 }
 
+// ============================================================ split-bf16 feed-forward
+// Both FF GEMMs take split-bf16 operands v = hi + lo (hi = bf16(v), lo = bf16(v - hi)) and form
+// hi.hi + hi.lo + lo.hi on the bf16 MFMA with fp32 accumulation; the dropped lo.lo term is ~2^-16
+// relative.  xn and the GELU output are split in registers, W1 and W2 carry packed lo parts, and the
+// out-projection stays bf16.  These four operands (W1, W2, xn into FF1, gelu(h)) are the rounding
+// points that dominate the error of the all-bf16 design.
+// One wave per SIMD: the hi and lo B operands of xn (128 registers) and the residual accumulators
+// (128) need the whole 512-entry register file, so a workgroup is 4 waves x 32 tokens.  FF stage k
+// holds W1 tile k (hi, lo) and the two W2 k-steps of hidden tile k-1 (hi, lo), 64 KB, so that FF1 of
+// tile k and the GELU of tile k-1 are independent work within one stage.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitFfStages = kFfStages + 1;
+
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pk_bf16(a, b);
+  lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
+template <bool OUTPROJ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mlp_split(
+    const uint16_t* __restrict__ O, const uint8_t* __restrict__ layer, float* __restrict__ X,
+    uint16_t* __restrict__ xn, int64_t n, float eps) {
+  __shared__ u32x4 lds[2][64 * 64];  // 2 stages x 64 operand blocks of 1 KB
+  const u32x4* wo = reinterpret_cast<const u32x4*>(layer + kOffOut);
+  const u32x4* w1 = reinterpret_cast<const u32x4*>(layer + kOffFf1);
+  const u32x4* w2 = reinterpret_cast<const u32x4*>(layer + kOffFf2);
+  const u32x4* w1l = reinterpret_cast<const u32x4*>(layer + kOffFf1Lo);
+  const u32x4* w2l = reinterpret_cast<const u32x4*>(layer + kOffFf2Lo);
+  const float* b1 = reinterpret_cast<const float*>(layer + kOffBff1);
+  const float* b2 = reinterpret_cast<const float*>(layer + kOffBff2);
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int j = lane & 31, hh = lane >> 5;
+  const int64_t tok = (int64_t(blockIdx.x) * kSplitWaves + wave) * 32 + j;
+  const bool valid = tok < n;  // lanes past the end work on the last token's row and store nothing
+  const int64_t trow = valid ? tok : n - 1;
+  float* xr = X + trow * kDim;
+  uint16_t* nr = xn + trow * kDim;
+
+  f32x16 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(xr + 32 * t + row_of_group(g, hh));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][4 * g + r] = x[r];
+    }
+
+  u32x4 xb[16], xl[16];  // FF1 B operands (xn in register order): hi and lo parts
+  auto split_xn = [&](float inv) {
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const int t = ks >> 1, g0 = 2 * (ks & 1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t hi, lo;
+        split_pair(acc[t][4 * g0 + 2 * q] * inv, acc[t][4 * g0 + 2 * q + 1] * inv, hi, lo);
+        xb[ks][q] = hi;
+        xl[ks][q] = lo;
+      }
+    }
+  };
+  auto add_b2 = [&]() {
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 32 * t + row_of_group(g, hh));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][4 * g + r] += b[r];
+      }
+  };
+
+  constexpr int s_begin = OUTPROJ ? 0 : kOutStages;
+  constexpr int s_end = kOutStages + kSplitFfStages;
+  auto issue = [&](int s, int buf) {
+    if (s < kOutStages) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int b = wave * 8 + i;  // 32 blocks: W_out tile b/4, k-step 4s + b%4
+        lds_load_block(wo + (int64_t(b >> 2) * 32 + 4 * s + (b & 3)) * 64, &lds[buf][b * 64], lane);
+      }
+    } else {
+      const int k = s - kOutStages;
+      // 64 blocks, 16 per wave: W1 hi and lo of tile k (k-steps 0..15), then W2 hi and lo of
+      // output tile bb/2, k-step 2(k-1) + bb%2 (hidden tile k-1).
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int b = wave * 16 + i, bb = b & 15;
+        if (b < 32) {
+          if (k < kFfStages)
+            lds_load_block((b < 16 ? w1 : w1l) + (int64_t(k) * 16 + bb) * 64, &lds[buf][b * 64], lane);
+        } else if (k > 0) {
+          lds_load_block((b < 48 ? w2 : w2l) + (int64_t(bb >> 1) * 64 + 2 * (k - 1) + (bb & 1)) * 64,
+                         &lds[buf][b * 64], lane);
+        }
+      }
+    }
+  };
+
+  if (!OUTPROJ) {
+    split_xn(acc_inv_norm(acc, eps));
+    add_b2();
+  }
+  const uint16_t* orow = O + trow * 512;
+  u32x4 ob[4];
+  auto load_o = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ob[i] = reinterpret_cast<const u32x4*>(orow)[2 * (4 * s + i) + hh];
+  };
+  if (OUTPROJ) load_o(0);
+  issue(s_begin, 0);
+
+  if (OUTPROJ) {
+    for (int s = 0; s < kOutStages; ++s) {
+      stage_barrier();
+      issue(s + 1, (s + 1) & 1);
+      const u32x4* Ls = lds[s & 1];
+      u32x4 cur[4] = {ob[0], ob[1], ob[2], ob[3]};
+      if (s + 1 < kOutStages) load_o(s + 1);
+#pragma unroll
+      for (int ksl = 0; ksl < 4; ++ksl)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = mfma32(Ls[(t * 4 + ksl) * 64 + lane], cur[ksl], acc[t]);
+    }
+    split_xn(acc_inv_norm(acc, eps));
+    add_b2();
+  }
+
+  f32x16 hs = zero16();  // FF1 of the previous hidden tile, before bias and GELU
+  for (int k = 0; k < kSplitFfStages; ++k) {
+    const int s = kOutStages + k;
+    f32x4 bias[4];
+    if (k > 0) {  // loaded before the next stage is issued, so waiting for it never waits for the stage
+#pragma unroll
+      for (int g = 0; g < 4; ++g) bias[g] = *reinterpret_cast<const f32x4*>(b1 + 32 * (k - 1) + row_of_group(g, hh));
+    }
+    stage_barrier();
+    if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
+    const u32x4* Ls = lds[s & 1];
+    f32x16 h0 = zero16(), h1 = zero16(), h2 = zero16();
+    if (k < kFfStages) {
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        const u32x4 a = Ls[ks * 64 + lane], al = Ls[(16 + ks) * 64 + lane];
+        h0 = mfma32(a, xb[ks], h0);
+        h1 = mfma32(a, xl[ks], h1);
+        h2 = mfma32(al, xb[ks], h2);
+      }
+    }
+    if (k > 0) {
+      u32x4 hb[2], hl[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r0 = 8 * c + 2 * q;
+          const float v0 = gelu_erf(hs[r0] + bias[r0 >> 2][r0 & 3]);
+          const float v1 = gelu_erf(hs[r0 + 1] + bias[(r0 + 1) >> 2][(r0 + 1) & 3]);
+          uint32_t hi, lo;
+          split_pair(v0, v1, hi, lo);
+          hb[c][q] = hi;
+          hl[c][q] = lo;
+        }
+#pragma unroll
+      for (int ot = 0; ot < 8; ++ot) {
+        const u32x4 a0 = Ls[(32 + 2 * ot) * 64 + lane], a1 = Ls[(33 + 2 * ot) * 64 + lane];
+        const u32x4 l0 = Ls[(48 + 2 * ot) * 64 + lane], l1 = Ls[(49 + 2 * ot) * 64 + lane];
+        acc[ot] = mfma32(a0, hb[0], acc[ot]);
+        acc[ot] = mfma32(a1, hb[1], acc[ot]);
+        acc[ot] = mfma32(a0, hl[0], acc[ot]);
+        acc[ot] = mfma32(a1, hl[1], acc[ot]);
+        acc[ot] = mfma32(l0, hb[0], acc[ot]);
+        acc[ot] = mfma32(l1, hb[1], acc[ot]);
+      }
+    }
+    if (k < kFfStages) hs = h0 + (h1 + h2);
+  }
+  const float inv = acc_inv_norm(acc, eps);
+  if (valid) store_row(acc, inv, xr, nr, hh);
+}
+
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
-                      float eps, hipStream_t st) {
+                      bool split_ff, float eps, hipStream_t st) {
+  if (with_ff && split_ff) {
+    const unsigned blocks = unsigned((n + 32 * kSplitWaves - 1) / (32 * kSplitWaves));
+    hipLaunchKernelGGL(k_mlp_split<true>, dim3(blocks), dim3(64 * kSplitWaves), 0, st, O, layer, X, xn, n, eps);
+    return;
+  }
   const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
   if (with_ff)
     hipLaunchKernelGGL((k_mlp<true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
@@ -918,7 +1105,13 @@ void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_
     hipLaunchKernelGGL((k_mlp<true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
 }
 
-void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, float eps, hipStream_t st) {
+void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool split_ff, float eps, hipStream_t st) {
+  if (split_ff) {
+    const unsigned blocks = unsigned((n + 32 * kSplitWaves - 1) / (32 * kSplitWaves));
+    hipLaunchKernelGGL(k_mlp_split<false>, dim3(blocks), dim3(64 * kSplitWaves), 0, st,
+                       static_cast<const uint16_t*>(nullptr), layer, X, xn, n, eps);
+    return;
+  }
   const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
   hipLaunchKernelGGL((k_mlp<false, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st,
                      static_cast<const uint16_t*>(nullptr), layer, X, xn, n, eps);

@@ -21,10 +21,12 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
 MODE_TIME, MODE_FREQ = 0, 1
+PREC_BF16, PREC_FF_SPLIT = 0, 1
+PRECISIONS = {"bf16": PREC_BF16, "ff_split": PREC_FF_SPLIT}
 _F32, _BF16 = 0, 1
 
 _lock = threading.Lock()
@@ -46,6 +48,8 @@ class TrfLayerSrc(ctypes.Structure):
         ("b_ff1", ctypes.c_void_p),
         ("w_ff2", ctypes.c_void_p),
         ("b_ff2", ctypes.c_void_p),
+        ("w_ff1_lo", ctypes.c_void_p),
+        ("w_ff2_lo", ctypes.c_void_p),
     ]
 
 
@@ -65,15 +69,16 @@ _SIGNATURES: dict[str, tuple] = {
     "trf_stack_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "trf_stack_forward": (
         ctypes.c_int,
-        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _P, _P, _P, _SZ, _P],
+        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P,
+         _SZ, _P],
     ),
     "trf_stack_forward_timed": (
         ctypes.c_int,
-        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _P, _P, _P, _SZ,
-         ctypes.POINTER(ctypes.c_void_p), _I32, _P],
+        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P,
+         _SZ, ctypes.POINTER(ctypes.c_void_p), _I32, _P],
     ),
     "trf_attn_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _P, _SZ, _P]),
-    "trf_ff_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _SZ, _P]),
+    "trf_ff_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _SZ, _P]),
 }
 
 
@@ -182,8 +187,18 @@ def workspace_bytes(batch: int, T: int, F: int) -> int:
 # ---------------------------------------------------------------------------------------------- ops
 
 
-def pack_layer(w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2, out: torch.Tensor) -> None:
-    """Pack plain folded weights (device, row-major) into ``out`` (uint8, layer_packed_bytes())."""
+def precision_code(precision: str) -> int:
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision must be one of {tuple(PRECISIONS)}, got {precision!r}")
+    return PRECISIONS[precision]
+
+
+def pack_layer(w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2, out: torch.Tensor, w_ff1_lo=None,
+               w_ff2_lo=None) -> None:
+    """Pack plain folded weights (device, row-major) into ``out`` (uint8, layer_packed_bytes()).
+
+    ``w_ff1_lo`` / ``w_ff2_lo``: optional bf16 residuals ``w - bf16(w)`` of the fp32 FF weights, for the
+    ``ff_split`` precision (zero when omitted)."""
     lib = load()
     _need(w_qkvg, "w_qkvg", torch.bfloat16, (QKVG_ROWS, DIM))
     _need(b_gate, "b_gate", torch.float32, (HEADS,))
@@ -193,7 +208,12 @@ def pack_layer(w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2, out: torch.Ten
     _need(w_ff2, "w_ff2", torch.bfloat16, (DIM, FF_HIDDEN))
     _need(b_ff2, "b_ff2", torch.float32, (DIM,))
     _need(out, "out", torch.uint8, (lib.trf_layer_packed_bytes(),))
-    src = TrfLayerSrc(*(t.data_ptr() for t in (w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2)))
+    if w_ff1_lo is not None:
+        _need(w_ff1_lo, "w_ff1_lo", torch.bfloat16, (FF_HIDDEN, DIM))
+    if w_ff2_lo is not None:
+        _need(w_ff2_lo, "w_ff2_lo", torch.bfloat16, (DIM, FF_HIDDEN))
+    src = TrfLayerSrc(*(t.data_ptr() for t in (w_qkvg, b_gate, w_out, w_ff1, b_ff1, w_ff2, b_ff2)),
+                      _ptr(w_ff1_lo), _ptr(w_ff2_lo))
     _check(lib.trf_pack_layer(ctypes.byref(src), out.data_ptr(), _stream()))
 
 
@@ -285,12 +305,16 @@ SLOTS = ("qkv_rope_gemm", "attention", "post_attention")  # trf_kernel_slot orde
 
 
 def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], rope_time, rope_freq, ws,
-                  events: list | None = None) -> None:
+                  events: list | None = None, precision: str = "bf16") -> None:
     """The whole stack on X [batch*T*F, 256] fp32, in place (fast.py:269-341).
+
+    ``precision``: ``"bf16"`` (every GEMM operand bf16, the reference kernels' arithmetic) or
+    ``"ff_split"`` (split-bf16 operands in the two FF GEMMs).
 
     ``events``: optional list of 2*5*len(layers) ``torch.cuda.Event`` (or None) recorded before/after
     each kernel (slot order ``SLOTS``), for per-kernel timing on the launch stream."""
     lib = load()
+    prec = precision_code(precision)
     _need(X, "X", torch.float32, (batch * T * F, DIM))
     _need(ws, "workspace", torch.uint8)
     nb = lib.trf_layer_packed_bytes()
@@ -307,7 +331,7 @@ def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], 
     if events is None:
         _check(
             lib.trf_stack_forward(
-                X.data_ptr(), batch, T, F, ptrs, mds, len(layers), _ptr(rope_time), _ptr(rope_freq),
+                X.data_ptr(), batch, T, F, ptrs, mds, len(layers), prec, _ptr(rope_time), _ptr(rope_freq),
                 ws.data_ptr(), ws.numel(), _stream(),
             )
         )
@@ -322,7 +346,7 @@ def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], 
     evs = (ctypes.c_void_p * len(handles))(*handles)
     _check(
         lib.trf_stack_forward_timed(
-            X.data_ptr(), batch, T, F, ptrs, mds, len(layers), _ptr(rope_time), _ptr(rope_freq),
+            X.data_ptr(), batch, T, F, ptrs, mds, len(layers), prec, _ptr(rope_time), _ptr(rope_freq),
             ws.data_ptr(), ws.numel(), evs, len(handles), _stream(),
         )
     )
@@ -339,10 +363,11 @@ def attn_block(X, batch, T, F, layer, mode, rope, ws) -> None:
     _check(lib.trf_attn_block(X.data_ptr(), batch, T, F, layer.data_ptr(), mode, rope.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
 
 
-def ff_block(X, batch, T, F, layer, ws) -> None:
+def ff_block(X, batch, T, F, layer, ws, precision: str = "bf16") -> None:
     """One feed-forward sub-layer X += ff(X) (model.py:142)."""
     lib = load()
+    prec = precision_code(precision)
     _need(X, "X", torch.float32, (batch * T * F, DIM))
     _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
     _need(ws, "workspace", torch.uint8)
-    _check(lib.trf_ff_block(X.data_ptr(), batch, T, F, layer.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
+    _check(lib.trf_ff_block(X.data_ptr(), batch, T, F, layer.data_ptr(), prec, ws.data_ptr(), ws.numel(), _stream()))
