@@ -196,23 +196,19 @@ int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream) {
   if (!src->b_gate || !src->b_ff1 || !src->b_ff2) return fail(TRF_ERR_ARG, "bias pointers must not be NULL");
   hipStream_t st = as_hip(stream);
   uint8_t* d = static_cast<uint8_t*>(dst);
-  trf::launch_pack(src->w_qkvg, trf::kQkvgRows, trf::kDim, false, d + trf::kOffQkvg, st);
+  trf::launch_pack(src->w_qkvg, trf::kQkvgRows, trf::kDim, trf::kPack32Natural, d + trf::kOffQkvg, st);
   trf::launch_copy_f32(src->b_gate, trf::kHeads, reinterpret_cast<float*>(d + trf::kOffBgate), st);
-  trf::launch_pack(src->w_out, trf::kDim, 512, false, d + trf::kOffOut, st);
-  trf::launch_pack(src->w_ff1, trf::kHidden, trf::kDim, true, d + trf::kOffFf1, st);
+  trf::launch_pack(src->w_out, trf::kDim, 512, trf::kPack32Natural, d + trf::kOffOut, st);
+  trf::launch_pack(src->w_ff1, trf::kHidden, trf::kDim, trf::kPack32RegOrder, d + trf::kOffFf1, st);
   trf::launch_copy_f32(src->b_ff1, trf::kHidden, reinterpret_cast<float*>(d + trf::kOffBff1), st);
-  trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, true, d + trf::kOffFf2, st);
+  trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, trf::kPack32RegOrder, d + trf::kOffFf2, st);
   trf::launch_copy_f32(src->b_ff2, trf::kDim, reinterpret_cast<float*>(d + trf::kOffBff2), st);
-  if (src->w_ff1_lo) {
-    trf::launch_pack(src->w_ff1_lo, trf::kHidden, trf::kDim, true, d + trf::kOffFf1Lo, st);
-  } else if (hipMemsetAsync(d + trf::kOffFf1Lo, 0, trf::kSzFf1, st) != hipSuccess) {
-    return check_launch("pack_layer (w_ff1_lo)");
-  }
-  if (src->w_ff2_lo) {
-    trf::launch_pack(src->w_ff2_lo, trf::kDim, trf::kHidden, true, d + trf::kOffFf2Lo, st);
-  } else if (hipMemsetAsync(d + trf::kOffFf2Lo, 0, trf::kSzFf2, st) != hipSuccess) {
-    return check_launch("pack_layer (w_ff2_lo)");
-  }
+  // operands of the split-bf16 feed-forward (16x16 tiles); absent lo parts pack as zeros
+  trf::launch_pack(src->w_out, trf::kDim, 512, trf::kPack16Natural, d + trf::kOffOut16, st);
+  trf::launch_pack(src->w_ff1, trf::kHidden, trf::kDim, trf::kPack16RegOrder, d + trf::kOffFf1Hi16, st);
+  trf::launch_pack(src->w_ff1_lo, trf::kHidden, trf::kDim, trf::kPack16RegOrder, d + trf::kOffFf1Lo16, st);
+  trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, trf::kPack16RegOrder, d + trf::kOffFf2Hi16, st);
+  trf::launch_pack(src->w_ff2_lo, trf::kDim, trf::kHidden, trf::kPack16RegOrder, d + trf::kOffFf2Lo16, st);
   return check_launch("pack_layer");
 }
 

@@ -34,10 +34,20 @@ constexpr size_t kOffBff1 = kOffFf1 + kSzFf1;
 constexpr size_t kOffFf2 = kOffBff1 + kHidden * 4;
 constexpr size_t kSzFf2 = size_t(kDim / 32) * (kHidden / 16) * kTileBytes;
 constexpr size_t kOffBff2 = kOffFf2 + kSzFf2;
-// Low parts of W1 and W2 (bf16(W - bf16(W))), same tiling, for the split-bf16 feed-forward.
-constexpr size_t kOffFf1Lo = kOffBff2 + kDim * 4;
-constexpr size_t kOffFf2Lo = kOffFf1Lo + kSzFf1;
-constexpr size_t kLayerBytes = kOffFf2Lo + kSzFf2;
+// The split-bf16 feed-forward runs on 16x16x32 MFMAs, whose A operand is 16 rows x 32 k: tiles
+// [rows/16][K/32][64 lanes][8 bf16], tile[t][ks][lane][e] = W[16t + lane%16][32ks + kperm16(lane/16, e)],
+// natural kperm16(g, e) = 8g + e (W_out), register order kperm16(g, e) = 16(e/4) + 4g + e%4 (W1, W2: a
+// 16x16 accumulator holds rows 4g..4g+3 in lane group g, so two tiles form one 32-deep B operand).
+// W1 and W2 come as hi = bf16(W) and lo = bf16(W - hi).
+constexpr size_t kOffOut16 = kOffBff2 + kDim * 4;
+constexpr size_t kOffFf1Hi16 = kOffOut16 + kSzOut;
+constexpr size_t kOffFf1Lo16 = kOffFf1Hi16 + kSzFf1;
+constexpr size_t kOffFf2Hi16 = kOffFf1Lo16 + kSzFf1;
+constexpr size_t kOffFf2Lo16 = kOffFf2Hi16 + kSzFf2;
+constexpr size_t kLayerBytes = kOffFf2Lo16 + kSzFf2;
+
+// Operand tile layouts of launch_pack.
+enum PackLayout { kPack32Natural = 0, kPack32RegOrder = 1, kPack16Natural = 2, kPack16RegOrder = 3 };
 
 inline int32_t seq_pad(int32_t L) { return (L + 63) / 64 * 64; }
 
@@ -55,7 +65,8 @@ inline SeqShape seq_shape(int mode, int batch, int T, int F) {
 }
 
 // Kernel launchers (trf_kernels.hip).  They only enqueue work; the caller checks errors.
-void launch_pack(const uint16_t* W, int rows, int K, bool reg_order, uint8_t* dst, hipStream_t st);
+// Pack W [rows][K] bf16 into MFMA A-operand tiles (layout: PackLayout); W == nullptr packs zeros.
+void launch_pack(const uint16_t* W, int rows, int K, int layout, uint8_t* dst, hipStream_t st);
 void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st);
 void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n,
                         float eps, hipStream_t st);

@@ -69,35 +69,47 @@ __device__ __forceinline__ int row_of_group(int g, int hh) { return 8 * g + 4 * 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ============================================================ weight packing
-// dst[t][ks][lane][e] = W[32t + lane%32][16ks + kperm(lane/32, e)], zero rows past `rows`
-// (kperm: natural 8hh + e, or register order 4hh + e / 8 + 4hh + e - 4; see trf_internal.h).
-__global__ void k_pack(const uint16_t* __restrict__ W, int rows, int K, int reg_order, u32x4* __restrict__ dst) {
-  const int ksteps = K / 16;
-  const int64_t total = int64_t((rows + 31) / 32) * ksteps * 64;
+// 32x32 layouts: dst[t][ks][lane][e] = W[32t + lane%32][16ks + kperm(lane/32, e)] (kperm: natural 8hh + e,
+// or register order 4hh + e / 8 + 4hh + e - 4).  16x16 layouts: dst[t][ks][lane][e] =
+// W[16t + lane%16][32ks + kperm16(lane/16, e)] (natural 8g + e, register order 16(e/4) + 4g + e%4).
+// Rows past `rows` are zero, and so is everything when W is null.  (See trf_internal.h.)
+__global__ void k_pack(const uint16_t* __restrict__ W, int rows, int K, int layout, u32x4* __restrict__ dst) {
+  const bool t16 = layout >= kPack16Natural;
+  const int tr = t16 ? 16 : 32, kstep = t16 ? 32 : 16;
+  const int ksteps = K / kstep;
+  const int64_t total = int64_t((rows + tr - 1) / tr) * ksteps * 64;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int lane = int(i % 64);
   const int ks = int((i / 64) % ksteps);
   const int t = int(i / (64 * ksteps));
-  const int row = 32 * t + (lane & 31);
-  const int hh = lane >> 5;
+  const int row = tr * t + lane % tr;
+  const int grp = lane / tr;
   u32x4 v = zero4();
-  if (row < rows) {
-    const uint16_t* src = W + int64_t(row) * K + 16 * ks;
-    if (reg_order) {
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(src + 4 * hh);
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8 + 4 * hh);
+  if (W && row < rows) {
+    const uint16_t* src = W + int64_t(row) * K + kstep * ks;
+    if (layout == kPack32Natural) {
+      v = *reinterpret_cast<const u32x4*>(src + 8 * grp);
+    } else if (layout == kPack32RegOrder) {
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(src + 4 * grp);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8 + 4 * grp);
       v = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    } else if (layout == kPack16Natural) {
+      v = *reinterpret_cast<const u32x4*>(src + 8 * grp);
     } else {
-      v = *reinterpret_cast<const u32x4*>(src + 8 * hh);
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(src + 4 * grp);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 16 + 4 * grp);
+      v = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
   }
   dst[i] = v;
 }
 
-void launch_pack(const uint16_t* W, int rows, int K, bool reg_order, uint8_t* dst, hipStream_t st) {
-  const int64_t total = int64_t((rows + 31) / 32) * (K / 16) * 64;
-  hipLaunchKernelGGL(k_pack, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, W, rows, K, int(reg_order),
+void launch_pack(const uint16_t* W, int rows, int K, int layout, uint8_t* dst, hipStream_t st) {
+  const bool t16 = layout >= kPack16Natural;
+  const int tr = t16 ? 16 : 32, kstep = t16 ? 32 : 16;
+  const int64_t total = int64_t((rows + tr - 1) / tr) * (K / kstep) * 64;
+  hipLaunchKernelGGL(k_pack, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, W, rows, K, layout,
                      reinterpret_cast<u32x4*>(dst));
 }
 
@@ -169,65 +181,29 @@ __device__ __forceinline__ void lds_load_block(const u32x4* __restrict__ src_blo
 // All of this thread's outstanding global loads (direct-to-LDS ones included) have landed, and every
 // wave of the workgroup has reached this point.
 __device__ __forceinline__ void stage_barrier() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15), as the builtin so that the compiler's own waitcnt
+  // insertion knows every earlier global load has landed (an inline-asm wait is opaque to it, and it
+  // would then wait again, for the next stage's loads too, at the first use of such a value).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 }
 
 // ============================================================ fused QKV + gate GEMM, rotary epilogue
 // One wave owns 32 consecutive padded positions of one sequence; its 32 tokens' xn rows stay in
-// registers as B operands.  The workgroup (8 waves) streams the 49 weight tiles (q heads 0-7 x 2, k, v,
-// gates) through LDS, two tiles per stage.  (kernels.cpp:439-540)
+// registers as B operands.  The workgroup (8 waves, 2 per SIMD) streams the 49 weight tiles through
+// LDS four per stage (13 stages: q heads, k heads, v heads, then the gate tile), so every stage is of
+// one kind and its four MFMA chains run interleaved.  The rotary cos/sin of the wave's position and
+// the gate biases are loaded into registers once.  (kernels.cpp:439-540)
 constexpr int kQkvWaves = 8;
-constexpr int kQkvStages = (kQkvgTiles + 1) / 2;
-
-__device__ __forceinline__ void qkv_epilogue(int t, const f32x16& acc, bool valid, int s, int p, int64_t tok, int hh,
-                                             int Lpad, const float* __restrict__ rc, const float* __restrict__ rs,
-                                             const float* __restrict__ bgate, uint16_t* __restrict__ Q,
-                                             uint16_t* __restrict__ K, uint16_t* __restrict__ Vt,
-                                             float* __restrict__ G) {
-  if (t < 32) {  // q or k: rotate interleaved pairs in fp32, store bf16 rows
-    const int h = (t & 15) >> 1;
-    uint16_t* dst = (t < 16 ? Q : K) + ((int64_t(s) * kHeads + h) * Lpad + p) * kHeadDim;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = 32 * (t & 1) + row_of_group(g, hh);
-      u32x2 o = {0u, 0u};
-      if (valid) {
-        const float c0 = rc[d0 >> 1], s0 = rs[d0 >> 1], c1 = rc[(d0 >> 1) + 1], s1 = rs[(d0 >> 1) + 1];
-        const float a0 = acc[4 * g], a1 = acc[4 * g + 1], a2 = acc[4 * g + 2], a3 = acc[4 * g + 3];
-        // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
-        const float sc = t < 16 ? kLog2e : 1.0f;
-        o[0] = pk_bf16(fmaf(a0, c0, -(a1 * s0)) * sc, fmaf(a1, c0, a0 * s0) * sc);
-        o[1] = pk_bf16(fmaf(a2, c1, -(a3 * s1)) * sc, fmaf(a3, c1, a2 * s1) * sc);
-      }
-      *reinterpret_cast<u32x2*>(dst + d0) = o;
-    }
-  } else if (t < 48) {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
-    const int h = (t - 32) >> 1;
-    uint16_t* dst = Vt + (int64_t(s) * kHeads + h) * kHeadDim * Lpad + p;
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 32 * (t & 1) + row_of_group(g, hh) + r;
-        dst[int64_t(d) * Lpad] = valid ? to_bf16(acc[4 * g + r]) : uint16_t(0);
-      }
-  } else if (valid) {  // gate rows 0..7 live in register group 0 of both half-waves
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int hd = 4 * hh + r;
-      const float z = acc[r] + bgate[hd];
-      G[tok * kHeads + hd] = 1.0f / (1.0f + expf(-z));
-    }
-  }
-}
+constexpr int kQkvTps = 4;
+constexpr int kQkvStages = (kQkvgTiles + kQkvTps - 1) / kQkvTps;
 
 __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
                                                   const float* __restrict__ bgate, const float* __restrict__ rope,
                                                   int mode, int nseq, int L, int Lpad, int T, int F,
                                                   uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
                                                   uint16_t* __restrict__ Vt, float* __restrict__ G) {
-  __shared__ u32x4 lds[2][2 * 16 * 64];  // 2 stages x 2 tiles x 16 k-steps x 1 KB
+  __shared__ u32x4 lds[2][kQkvTps * 16 * 64];  // 2 stages x 4 tiles x 16 k-steps x 1 KB
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int64_t row0 = (int64_t(blockIdx.x) * kQkvWaves + wave) * 32;
@@ -243,14 +219,27 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
   }
-  const float* rc = rope + int64_t(valid ? p : 0) * 32;  // cos row
-  const float* rs = rc + int64_t(L) * 32;                // sin row
-
-  auto issue = [&](int stage, int buf) {
+  // Rotary of this position: features d0 = 32 half + 8g + 4hh (+0..3) form the pairs
+  // i = 16 half + 4g + 2hh + c, c = 0, 1.  rope = [cos | sin] rows of 32.
+  float2 rc[2][4], rsn[2][4];
+  {
+    const float* cr = rope + int64_t(valid ? p : 0) * 32;
+    const float* sr = cr + int64_t(L) * 32;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int b = wave * 4 + i;  // 32 blocks per stage: tile 2*stage + b/16, k-step b%16
-      const int t = 2 * stage + (b >> 4);
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        rc[half][g] = *reinterpret_cast<const float2*>(cr + 16 * half + 4 * g + 2 * hh);
+        rsn[half][g] = *reinterpret_cast<const float2*>(sr + 16 * half + 4 * g + 2 * hh);
+      }
+  }
+  const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
+
+  auto issue = [&](int stage, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int b = wave * 8 + i;  // 64 blocks per stage: tile 4*stage + b/16, k-step b%16
+      const int t = kQkvTps * stage + (b >> 4);
       if (t < kQkvgTiles) lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, &lds[buf][b * 64], lane);
     }
   };
@@ -260,14 +249,74 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
     if (stage + 1 < kQkvStages) issue(stage + 1, (stage + 1) & 1);
     if (!active) continue;
     const u32x4* Ls = lds[stage & 1];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int t = 2 * stage + tt;
-      if (t >= kQkvgTiles) break;
+    if (stage == kQkvStages - 1) {  // the gate tile: rows 0..7 live in register group 0 of both half-waves
       f32x16 acc = zero16();
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) acc = mfma32(Ls[(tt * 16 + ks) * 64 + lane], bx[ks], acc);
-      qkv_epilogue(t, acc, valid, s, p, tok, hh, Lpad, rc, rs, bgate, Q, K, Vt, G);
+      for (int ks = 0; ks < 16; ++ks) acc = mfma32(Ls[ks * 64 + lane], bx[ks], acc);
+      if (valid) {
+        f32x4 gv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gv[r] = 1.0f / (1.0f + expf(-(acc[r] + bg[r])));
+        *reinterpret_cast<f32x4*>(G + tok * kHeads + 4 * hh) = gv;
+      }
+      continue;
+    }
+    f32x16 acc[kQkvTps];
+    u32x4 a[kQkvTps];
+#pragma unroll
+    for (int tt = 0; tt < kQkvTps; ++tt) {
+      acc[tt] = zero16();
+      a[tt] = Ls[tt * 16 * 64 + lane];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {  // operands of k-step ks+1 are read while ks multiplies
+      u32x4 an[kQkvTps];
+#pragma unroll
+      for (int tt = 0; tt < kQkvTps; ++tt)
+        if (ks + 1 < 16) an[tt] = Ls[(tt * 16 + ks + 1) * 64 + lane];
+#pragma unroll
+      for (int tt = 0; tt < kQkvTps; ++tt) acc[tt] = mfma32(a[tt], bx[ks], acc[tt]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tt = 0; tt < kQkvTps; ++tt)
+        if (ks + 1 < 16) a[tt] = an[tt];
+    }
+    if (stage < 8) {  // q (stages 0-3) or k (4-7): rotate interleaved pairs in fp32, store bf16 rows
+      // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
+      const float sc = stage < 4 ? kLog2e : 1.0f;
+      uint16_t* base = stage < 4 ? Q : K;
+#pragma unroll
+      for (int tt = 0; tt < kQkvTps; ++tt) {
+        const int t = kQkvTps * stage + tt, h = (t & 15) >> 1, half = tt & 1;
+        uint16_t* dst = base + ((int64_t(s) * kHeads + h) * Lpad + p) * kHeadDim;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * half + row_of_group(g, hh);
+          const float2 c = rc[half][g], sn = rsn[half][g];
+          const float a0 = acc[tt][4 * g], a1 = acc[tt][4 * g + 1], a2 = acc[tt][4 * g + 2], a3 = acc[tt][4 * g + 3];
+          u32x2 o = {0u, 0u};
+          if (valid) {
+            o[0] = pk_bf16(fmaf(a0, c.x, -(a1 * sn.x)) * sc, fmaf(a1, c.x, a0 * sn.x) * sc);
+            o[1] = pk_bf16(fmaf(a2, c.y, -(a3 * sn.y)) * sc, fmaf(a3, c.y, a2 * sn.y) * sc);
+          }
+          *reinterpret_cast<u32x2*>(dst + d0) = o;
+        }
+      }
+    } else {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
+      // per-lane base (sequence, half-wave rows, position); every row offset below is wave-uniform
+      uint16_t* vb = Vt + int64_t(s) * kHeads * kHeadDim * Lpad + int64_t(4 * hh) * Lpad + p;
+#pragma unroll
+      for (int tt = 0; tt < kQkvTps; ++tt) {
+        const int t = kQkvTps * stage + tt, h = (t - 32) >> 1, half = tt & 1;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int drow = h * kHeadDim + 32 * half + 8 * g + r;  // row of V^T, less 4hh
+            vb[int64_t(__builtin_amdgcn_readfirstlane(drow * Lpad))] =
+                valid ? to_bf16(acc[tt][4 * g + r]) : uint16_t(0);
+          }
+      }
     }
   }
 }
@@ -915,187 +964,209 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
 // relative.  xn and the GELU output are split in registers, W1 and W2 carry packed lo parts, and the
 // out-projection stays bf16.  These four operands (W1, W2, xn into FF1, gelu(h)) are the rounding
 // points that dominate the error of the all-bf16 design.
-// One wave per SIMD: the hi and lo B operands of xn (128 registers) and the residual accumulators
-// (128) need the whole 512-entry register file, so a workgroup is 4 waves x 32 tokens.  FF stage k
-// holds W1 tile k (hi, lo) and the two W2 k-steps of hidden tile k-1 (hi, lo), 64 KB, so that FF1 of
-// tile k and the GELU of tile k-1 are independent work within one stage.
-constexpr int kSplitWaves = 4;
-constexpr int kSplitFfStages = kFfStages + 1;
+//
+// Shape: v_mfma_f32_16x16x32_bf16 with 16 tokens per wave (output features on the 16 rows, tokens on
+// the 16 columns; lane l holds token l%16 and rows 4(l/16)..+3 of a tile).  The residual stream is 16
+// tiles x 4 registers and the hi and lo B operands of xn 2 x 32 registers, so a wave fits in 256
+// registers and two waves share each SIMD: one wave's GELU runs while the other's MFMAs do.  A
+// workgroup is 4 waves (64 tokens) with 2 x 32 KB of LDS stages, two workgroups per CU.
+// Stages: 0..7 out-projection (W_out k-steps 2s, 2s+1 of all 16 tiles); then for each block j of 32
+// hidden units, stage A_j = W1 hi and lo of tiles 2j, 2j+1 (FF1), and stage B_j = W2 hi and lo of
+// k-step j of all 16 output tiles (GELU of block j, FF2).
+constexpr int kX3Waves = 4;
+constexpr int kX3OutStages = 8;
+constexpr int kX3Blocks = kHidden / 32;
+constexpr int kX3Stages = kX3OutStages + 2 * kX3Blocks;
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4f() {
+  f32x4 z = {};
+  return z;
+}
 
 __device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
   hi = pk_bf16(a, b);
   lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 
+// Register-order B operand from two 16x16 accumulator tiles (values scaled by s): element pairs
+// (tile u, rows 2q', 2q'+1) in the order of kperm16 = 16(e/4) + 4g + e%4.
+__device__ __forceinline__ void split_operand(const f32x4& t0, const f32x4& t1, float s, u32x4& hi, u32x4& lo) {
+  uint32_t h, l;
+  split_pair(t0[0] * s, t0[1] * s, h, l);
+  hi[0] = h;
+  lo[0] = l;
+  split_pair(t0[2] * s, t0[3] * s, h, l);
+  hi[1] = h;
+  lo[1] = l;
+  split_pair(t1[0] * s, t1[1] * s, h, l);
+  hi[2] = h;
+  lo[2] = l;
+  split_pair(t1[2] * s, t1[3] * s, h, l);
+  hi[3] = h;
+  lo[3] = l;
+}
+
+struct X3Weights {
+  const u32x4* wo;   // W_out, 16x16 natural: [16 tiles][16 k-steps]
+  const u32x4* w1h;  // W1 hi / lo, 16x16 register order: [64 tiles][8 k-steps]
+  const u32x4* w1l;
+  const u32x4* w2h;  // W2 hi / lo, 16x16 register order: [16 tiles][32 k-steps]
+  const u32x4* w2l;
+};
+
+// This wave's 8 of the stage's 32 blocks into LDS buffer dst.
+__device__ __forceinline__ void x3_issue(const X3Weights& w, int s, u32x4* dst, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int b = wave * 8 + i;
+    const u32x4* src;
+    if (s < kX3OutStages) {
+      src = w.wo + (int64_t(b >> 1) * 16 + 2 * s + (b & 1)) * 64;  // tile b/2, k-step 2s + b%2
+    } else {
+      const int u = s - kX3OutStages, j = u >> 1;
+      if ((u & 1) == 0)  // A_j: part b/16 (hi, lo), tile 2j + (b/8)%2, k-step b%8
+        src = ((b < 16) ? w.w1h : w.w1l) + (int64_t(2 * j + ((b >> 3) & 1)) * 8 + (b & 7)) * 64;
+      else  // B_j: part b/16, output tile b%16, k-step j
+        src = ((b < 16) ? w.w2h : w.w2l) + (int64_t(b & 15) * 32 + j) * 64;
+    }
+    lds_load_block(src, dst + b * 64, lane);
+  }
+}
+
 template <bool OUTPROJ>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mlp_split(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_mlp_x3(
     const uint16_t* __restrict__ O, const uint8_t* __restrict__ layer, float* __restrict__ X,
     uint16_t* __restrict__ xn, int64_t n, float eps) {
-  __shared__ u32x4 lds[2][64 * 64];  // 2 stages x 64 operand blocks of 1 KB
-  const u32x4* wo = reinterpret_cast<const u32x4*>(layer + kOffOut);
-  const u32x4* w1 = reinterpret_cast<const u32x4*>(layer + kOffFf1);
-  const u32x4* w2 = reinterpret_cast<const u32x4*>(layer + kOffFf2);
-  const u32x4* w1l = reinterpret_cast<const u32x4*>(layer + kOffFf1Lo);
-  const u32x4* w2l = reinterpret_cast<const u32x4*>(layer + kOffFf2Lo);
+  __shared__ u32x4 lds[2][32 * 64];  // 2 stages x 32 operand blocks of 1 KB
+  X3Weights w;
+  w.wo = reinterpret_cast<const u32x4*>(layer + kOffOut16);
+  w.w1h = reinterpret_cast<const u32x4*>(layer + kOffFf1Hi16);
+  w.w1l = reinterpret_cast<const u32x4*>(layer + kOffFf1Lo16);
+  w.w2h = reinterpret_cast<const u32x4*>(layer + kOffFf2Hi16);
+  w.w2l = reinterpret_cast<const u32x4*>(layer + kOffFf2Lo16);
   const float* b1 = reinterpret_cast<const float*>(layer + kOffBff1);
   const float* b2 = reinterpret_cast<const float*>(layer + kOffBff2);
   const int lane = threadIdx.x & 63, wave = wave_id();
-  const int j = lane & 31, hh = lane >> 5;
-  const int64_t tok = (int64_t(blockIdx.x) * kSplitWaves + wave) * 32 + j;
+  const int col = lane & 15, g = lane >> 4;
+  const int64_t tok = (int64_t(blockIdx.x) * kX3Waves + wave) * 16 + col;
   const bool valid = tok < n;  // lanes past the end work on the last token's row and store nothing
   const int64_t trow = valid ? tok : n - 1;
   float* xr = X + trow * kDim;
   uint16_t* nr = xn + trow * kDim;
 
-  f32x16 acc[8];
+  f32x4 acc[16];  // residual stream: tile t holds features 16t + 4g + r of this lane's token
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(xr + 32 * t + row_of_group(g, hh));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][4 * g + r] = x[r];
-    }
+  for (int t = 0; t < 16; ++t) acc[t] = *reinterpret_cast<const f32x4*>(xr + 16 * t + 4 * g);
 
-  u32x4 xb[16], xl[16];  // FF1 B operands (xn in register order): hi and lo parts
-  auto split_xn = [&](float inv) {
+  auto inv_norm = [&]() __attribute__((always_inline)) {
+    float ss = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-      const int t = ks >> 1, g0 = 2 * (ks & 1);
+    for (int t = 0; t < 16; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t hi, lo;
-        split_pair(acc[t][4 * g0 + 2 * q] * inv, acc[t][4 * g0 + 2 * q + 1] * inv, hi, lo);
-        xb[ks][q] = hi;
-        xl[ks][q] = lo;
-      }
-    }
-  };
-  auto add_b2 = [&]() {
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 32 * t + row_of_group(g, hh));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][4 * g + r] += b[r];
-      }
+      for (int r = 0; r < 4; ++r) ss = fmaf(acc[t][r], acc[t][r], ss);
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    return 1.0f / fmaxf(sqrtf(ss), eps);
   };
 
-  constexpr int s_begin = OUTPROJ ? 0 : kOutStages;
-  constexpr int s_end = kOutStages + kSplitFfStages;
-  auto issue = [&](int s, int buf) {
-    if (s < kOutStages) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int b = wave * 8 + i;  // 32 blocks: W_out tile b/4, k-step 4s + b%4
-        lds_load_block(wo + (int64_t(b >> 2) * 32 + 4 * s + (b & 3)) * 64, &lds[buf][b * 64], lane);
-      }
-    } else {
-      const int k = s - kOutStages;
-      // 64 blocks, 16 per wave: W1 hi and lo of tile k (k-steps 0..15), then W2 hi and lo of
-      // output tile bb/2, k-step 2(k-1) + bb%2 (hidden tile k-1).
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int b = wave * 16 + i, bb = b & 15;
-        if (b < 32) {
-          if (k < kFfStages)
-            lds_load_block((b < 16 ? w1 : w1l) + (int64_t(k) * 16 + bb) * 64, &lds[buf][b * 64], lane);
-        } else if (k > 0) {
-          lds_load_block((b < 48 ? w2 : w2l) + (int64_t(bb >> 1) * 64 + 2 * (k - 1) + (bb & 1)) * 64,
-                         &lds[buf][b * 64], lane);
-        }
-      }
-    }
-  };
-
-  if (!OUTPROJ) {
-    split_xn(acc_inv_norm(acc, eps));
-    add_b2();
-  }
-  const uint16_t* orow = O + trow * 512;
-  u32x4 ob[4];
-  auto load_o = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ob[i] = reinterpret_cast<const u32x4*>(orow)[2 * (4 * s + i) + hh];
-  };
-  if (OUTPROJ) load_o(0);
-  issue(s_begin, 0);
-
+  int s0 = OUTPROJ ? 0 : kX3OutStages;
+  x3_issue(w, s0, lds[0], wave, lane);
   if (OUTPROJ) {
-    for (int s = 0; s < kOutStages; ++s) {
+    const u32x4* orow = reinterpret_cast<const u32x4*>(O + trow * 512);
+    u32x4 ob[2] = {orow[g], orow[4 + g]};  // k-steps 0, 1: O features 32ks + 8g..+7
+    for (int s = 0; s < kX3OutStages; ++s) {
       stage_barrier();
-      issue(s + 1, (s + 1) & 1);
+      x3_issue(w, s + 1, lds[(s + 1) & 1], wave, lane);
       const u32x4* Ls = lds[s & 1];
-      u32x4 cur[4] = {ob[0], ob[1], ob[2], ob[3]};
-      if (s + 1 < kOutStages) load_o(s + 1);
+      const u32x4 cur[2] = {ob[0], ob[1]};
+      if (s + 1 < kX3OutStages) {
+        ob[0] = orow[4 * (2 * s + 2) + g];
+        ob[1] = orow[4 * (2 * s + 3) + g];
+      }
 #pragma unroll
-      for (int ksl = 0; ksl < 4; ++ksl)
+      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) acc[t] = mfma32(Ls[(t * 4 + ksl) * 64 + lane], cur[ksl], acc[t]);
+        for (int t = 0; t < 16; ++t) acc[t] = mfma16(Ls[(2 * t + kk) * 64 + lane], cur[kk], acc[t]);
     }
-    split_xn(acc_inv_norm(acc, eps));
-    add_b2();
+  }
+  u32x4 xb[8], xl[8];  // FF1 B operands: xn hi and lo, k-step ks = tiles 2ks, 2ks+1 in register order
+  {
+    const float inv = inv_norm();
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) split_operand(acc[2 * ks], acc[2 * ks + 1], inv, xb[ks], xl[ks]);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 16 * t + 4 * g);
+      acc[t] += b;
+    }
   }
 
-  f32x16 hs = zero16();  // FF1 of the previous hidden tile, before bias and GELU
-  for (int k = 0; k < kSplitFfStages; ++k) {
-    const int s = kOutStages + k;
-    f32x4 bias[4];
-    if (k > 0) {  // loaded before the next stage is issued, so waiting for it never waits for the stage
-#pragma unroll
-      for (int g = 0; g < 4; ++g) bias[g] = *reinterpret_cast<const f32x4*>(b1 + 32 * (k - 1) + row_of_group(g, hh));
-    }
+  f32x4 hs[2];  // FF1 of the current hidden block (tiles 2j, 2j+1), before bias and GELU
+  for (int j = 0; j < kX3Blocks; ++j) {
+    const int s = kX3OutStages + 2 * j;
+    // stage A_j: FF1 of hidden tiles 2j, 2j+1
     stage_barrier();
-    if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
-    const u32x4* Ls = lds[s & 1];
-    f32x16 h0 = zero16(), h1 = zero16(), h2 = zero16();
-    if (k < kFfStages) {
+    x3_issue(w, s + 1, lds[(s + 1) & 1], wave, lane);
+    {
+      const u32x4* Ls = lds[s & 1];
+      f32x4 h0[2] = {zero4f(), zero4f()}, h1[2] = {zero4f(), zero4f()};
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {
-        const u32x4 a = Ls[ks * 64 + lane], al = Ls[(16 + ks) * 64 + lane];
-        h0 = mfma32(a, xb[ks], h0);
-        h1 = mfma32(a, xl[ks], h1);
-        h2 = mfma32(al, xb[ks], h2);
-      }
-    }
-    if (k > 0) {
-      u32x4 hb[2], hl[2];
+      for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r0 = 8 * c + 2 * q;
-          const float v0 = gelu_erf(hs[r0] + bias[r0 >> 2][r0 & 3]);
-          const float v1 = gelu_erf(hs[r0 + 1] + bias[(r0 + 1) >> 2][(r0 + 1) & 3]);
-          uint32_t hi, lo;
-          split_pair(v0, v1, hi, lo);
-          hb[c][q] = hi;
-          hl[c][q] = lo;
+        for (int u = 0; u < 2; ++u) {
+          const u32x4 a = Ls[(8 * u + ks) * 64 + lane], al = Ls[(16 + 8 * u + ks) * 64 + lane];
+          h0[u] = mfma16(a, xb[ks], h0[u]);
+          h1[u] = mfma16(a, xl[ks], h1[u]);
+          h0[u] = mfma16(al, xb[ks], h0[u]);
         }
+      hs[0] = h0[0] + h1[0];
+      hs[1] = h0[1] + h1[1];
+    }
+    // stage B_j: GELU of block j, then FF2 k-step j into every output tile
+    const f32x4 bb0 = *reinterpret_cast<const f32x4*>(b1 + 32 * j + 4 * g);
+    const f32x4 bb1 = *reinterpret_cast<const f32x4*>(b1 + 32 * j + 16 + 4 * g);
+    stage_barrier();
+    if (s + 2 < kX3Stages) x3_issue(w, s + 2, lds[s & 1], wave, lane);
+    {
+      const u32x4* Ls = lds[(s + 1) & 1];
+      f32x4 v0, v1;
 #pragma unroll
-      for (int ot = 0; ot < 8; ++ot) {
-        const u32x4 a0 = Ls[(32 + 2 * ot) * 64 + lane], a1 = Ls[(33 + 2 * ot) * 64 + lane];
-        const u32x4 l0 = Ls[(48 + 2 * ot) * 64 + lane], l1 = Ls[(49 + 2 * ot) * 64 + lane];
-        acc[ot] = mfma32(a0, hb[0], acc[ot]);
-        acc[ot] = mfma32(a1, hb[1], acc[ot]);
-        acc[ot] = mfma32(a0, hl[0], acc[ot]);
-        acc[ot] = mfma32(a1, hl[1], acc[ot]);
-        acc[ot] = mfma32(l0, hb[0], acc[ot]);
-        acc[ot] = mfma32(l1, hb[1], acc[ot]);
+      for (int r = 0; r < 4; ++r) {
+        v0[r] = gelu_erf(hs[0][r] + bb0[r]);
+        v1[r] = gelu_erf(hs[1][r] + bb1[r]);
+      }
+      u32x4 hb, hl;
+      split_operand(v0, v1, 1.0f, hb, hl);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const u32x4 a = Ls[t * 64 + lane], al = Ls[(16 + t) * 64 + lane];
+        acc[t] = mfma16(a, hb, acc[t]);
+        acc[t] = mfma16(a, hl, acc[t]);
+        acc[t] = mfma16(al, hb, acc[t]);
       }
     }
-    if (k < kFfStages) hs = h0 + (h1 + h2);
   }
-  const float inv = acc_inv_norm(acc, eps);
-  if (valid) store_row(acc, inv, xr, nr, hh);
+  const float inv = inv_norm();
+  if (valid) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      *reinterpret_cast<f32x4*>(xr + 16 * t + 4 * g) = acc[t];
+      const u32x2 v = {pk_bf16(acc[t][0] * inv, acc[t][1] * inv), pk_bf16(acc[t][2] * inv, acc[t][3] * inv)};
+      *reinterpret_cast<u32x2*>(nr + 16 * t + 4 * g) = v;
+    }
+  }
 }
 
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
                       bool split_ff, float eps, hipStream_t st) {
   if (with_ff && split_ff) {
-    const unsigned blocks = unsigned((n + 32 * kSplitWaves - 1) / (32 * kSplitWaves));
-    hipLaunchKernelGGL(k_mlp_split<true>, dim3(blocks), dim3(64 * kSplitWaves), 0, st, O, layer, X, xn, n, eps);
+    const unsigned blocks = unsigned((n + 16 * kX3Waves - 1) / (16 * kX3Waves));
+    hipLaunchKernelGGL(k_mlp_x3<true>, dim3(blocks), dim3(64 * kX3Waves), 0, st, O, layer, X, xn, n, eps);
     return;
   }
   const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
@@ -1107,8 +1178,8 @@ void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_
 
 void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool split_ff, float eps, hipStream_t st) {
   if (split_ff) {
-    const unsigned blocks = unsigned((n + 32 * kSplitWaves - 1) / (32 * kSplitWaves));
-    hipLaunchKernelGGL(k_mlp_split<false>, dim3(blocks), dim3(64 * kSplitWaves), 0, st,
+    const unsigned blocks = unsigned((n + 16 * kX3Waves - 1) / (16 * kX3Waves));
+    hipLaunchKernelGGL(k_mlp_x3<false>, dim3(blocks), dim3(64 * kX3Waves), 0, st,
                        static_cast<const uint16_t*>(nullptr), layer, X, xn, n, eps);
     return;
   }
