@@ -371,7 +371,7 @@ __device__ __forceinline__ void softmax_block(const f32x16& sacc, int key0, int 
 __device__ __forceinline__ float block_max(const f32x16& sacc, int key0, int L, int hh, float m) {
   if (key0 + 32 <= L) {
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) m = fmaxf(m, fmaxf(sacc[r], sacc[r + 1]));  // v_max3_f32
+    for (int r = 0; r < 16; r += 2) m = fmaxf(fmaxf(m, sacc[r]), sacc[r + 1]);  // one v_max3_f32 per pair
   } else {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
@@ -469,10 +469,12 @@ __device__ __forceinline__ void attn_max_tile(const u32x4* __restrict__ Kl, cons
 }
 
 // Pass-2 work of one 64-key tile: scores, exact-softmax probabilities, P.V accumulation.
+// The score accumulators start at -m (negm: the row max of this lane's query in all 16 registers),
+// so the MFMAs deliver s - m and the softmax needs no subtraction.
 template <bool MASK>
 __device__ __forceinline__ void attn_pv_tile(const u32x4* __restrict__ Kl, const u32x4* __restrict__ Vl,
                                              const u32x4 (&qb)[kAttQT][4], int key0, int L, int j, int hh,
-                                             const float (&m)[kAttQT], float (&lsum)[kAttQT],
+                                             const f32x16 (&negm)[kAttQT], float (&lsum)[kAttQT],
                                              f32x16 (&o)[kAttQT][2]) {
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
@@ -481,10 +483,10 @@ __device__ __forceinline__ void attn_pv_tile(const u32x4* __restrict__ Kl, const
     u32x4 p0[kAttQT], p1[kAttQT];
 #pragma unroll
     for (int qt = 0; qt < kAttQT; ++qt) {
-      f32x16 sacc = zero16();
+      f32x16 sacc = negm[qt];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[qt][ks], sacc);
-      softmax_block(sacc, MASK ? key0 + 32 * kh : 0, MASK ? L : 32, hh, m[qt], lsum[qt], p0[qt], p1[qt]);
+      softmax_block(sacc, MASK ? key0 + 32 * kh : 0, MASK ? L : 32, hh, 0.0f, lsum[qt], p0[qt], p1[qt]);
     }
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -500,11 +502,28 @@ __device__ __forceinline__ void attn_pv_tile(const u32x4* __restrict__ Kl, const
   }
 }
 
+// K/V tiles stream through a ring of kAttBufs LDS buffers, prefetched kAttBufs-1 tiles ahead.  Tile kt
+// is ready once at most the loads of the tiles issued after it are outstanding (N per tile per wave:
+// 2 for a K tile, 4 for K + V), and the barrier makes every wave's share visible.
+constexpr int kAttBufs = 3;
+
+// The wait is explicit, so the barrier is the bare s_barrier: __syncthreads' release fence would also
+// wait for the younger tiles' LDS-DMA loads.  The empty asm with a memory clobber keeps the compiler
+// from moving LDS accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void tile_barrier() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);  // vmcnt(N) expcnt(7) lgkmcnt(15)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ Vt, const float* __restrict__ G,
                                                    uint16_t* __restrict__ O, int mode, int L, int Lpad, int T,
                                                    int F, int nqb) {
-  __shared__ u32x4 lds[2][2][64 * 8];  // [buffer][K, V^T][64 rows x 8 chunks]
+  __shared__ u32x4 lds[kAttBufs][2][64 * 8];  // [buffer][K, V^T][64 rows x 8 chunks]
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs (8 L2 caches), so block b runs on
@@ -533,37 +552,55 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   float m[kAttQT];
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt) m[qt] = -INFINITY;
-  stage_k_tile(Kh, 0, lds[0][0], wave, lane);
-  for (int kt = 0; kt < nkt - 1; ++kt) {
-    stage_barrier();
-    stage_k_tile(Kh, kt + 1, lds[(kt + 1) & 1][0], wave, lane);
-    if (active) attn_max_tile<false>(lds[kt & 1][0], qb, 0, L, j, hh, m);
+#pragma unroll
+  for (int i = 0; i < kAttBufs - 1; ++i)
+    if (i < nkt) stage_k_tile(Kh, i, lds[i][0], wave, lane);
+  for (int kt = 0; kt < nkt; ++kt) {
+    if (kt + 1 < nkt)
+      tile_barrier<2>();
+    else
+      tile_barrier<0>();
+    if (kt + kAttBufs - 1 < nkt) stage_k_tile(Kh, kt + kAttBufs - 1, lds[(kt + kAttBufs - 1) % kAttBufs][0], wave, lane);
+    if (!active) continue;
+    if (kt + 1 < nkt)
+      attn_max_tile<false>(lds[kt % kAttBufs][0], qb, 0, L, j, hh, m);
+    else
+      attn_max_tile<true>(lds[kt % kAttBufs][0], qb, kt * 64, L, j, hh, m);
   }
-  stage_barrier();
-  if (active) attn_max_tile<true>(lds[(nkt - 1) & 1][0], qb, (nkt - 1) * 64, L, j, hh, m);
   float lsum[kAttQT];
+  f32x16 negm[kAttQT];
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt) {
     m[qt] = fmaxf(m[qt], __shfl_xor(m[qt], 32));
     lsum[qt] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negm[qt][r] = -m[qt];
   }
 
   // ---- pass 2: probabilities and P.V
   f32x16 o[kAttQT][2];
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt) o[qt][0] = o[qt][1] = zero16();
-  stage_barrier();  // everyone is done with the pass-1 buffers before they are overwritten
-  stage_k_tile(Kh, 0, lds[0][0], wave, lane);
-  stage_v_tile(Vh, 0, Lpad, lds[0][1], wave, lane);
+  tile_barrier<0>();  // everyone is done with the pass-1 buffers before they are overwritten
+#pragma unroll
+  for (int i = 0; i < kAttBufs - 1; ++i)
+    if (i < nkt) {
+      stage_k_tile(Kh, i, lds[i][0], wave, lane);
+      stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
+    }
   for (int kt = 0; kt < nkt - 1; ++kt) {
-    stage_barrier();
-    stage_k_tile(Kh, kt + 1, lds[(kt + 1) & 1][0], wave, lane);
-    stage_v_tile(Vh, kt + 1, Lpad, lds[(kt + 1) & 1][1], wave, lane);
-    if (active) attn_pv_tile<false>(lds[kt & 1][0], lds[kt & 1][1], qb, 0, L, j, hh, m, lsum, o);
+    tile_barrier<4>();
+    if (kt + kAttBufs - 1 < nkt) {
+      const int b = (kt + kAttBufs - 1) % kAttBufs;
+      stage_k_tile(Kh, kt + kAttBufs - 1, lds[b][0], wave, lane);
+      stage_v_tile(Vh, kt + kAttBufs - 1, Lpad, lds[b][1], wave, lane);
+    }
+    if (active) attn_pv_tile<false>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negm, lsum, o);
   }
-  stage_barrier();
+  tile_barrier<0>();
   if (!active) return;
-  attn_pv_tile<true>(lds[(nkt - 1) & 1][0], lds[(nkt - 1) & 1][1], qb, (nkt - 1) * 64, L, j, hh, m, lsum, o);
+  attn_pv_tile<true>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L, j, hh,
+                     negm, lsum, o);
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt)
     attn_store(o[qt], q0 + 32 * qt + j, L, s, h, hh, mode, T, F, G, lsum[qt] + __shfl_xor(lsum[qt], 32), O);
