@@ -556,8 +556,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   for (int i = 0; i < kAttBufs - 1; ++i)
     if (i < nkt) stage_k_tile(Kh, i, lds[i][0], wave, lane);
   for (int kt = 0; kt < nkt; ++kt) {
-    if (kt + 1 < nkt)
-      tile_barrier<2>();
+    if (kt + kAttBufs - 2 < nkt)  // the younger tiles kt+1 .. kt+kAttBufs-2 are in flight: 2 loads each
+      tile_barrier<2 * (kAttBufs - 2)>();
     else
       tile_barrier<0>();
     if (kt + kAttBufs - 1 < nkt) stage_k_tile(Kh, kt + kAttBufs - 1, lds[(kt + kAttBufs - 1) % kAttBufs][0], wave, lane);
@@ -589,7 +589,10 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
       stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
     }
   for (int kt = 0; kt < nkt - 1; ++kt) {
-    tile_barrier<4>();
+    if (kt + kAttBufs - 2 < nkt)  // K and V: 4 loads per younger tile in flight
+      tile_barrier<4 * (kAttBufs - 2)>();
+    else
+      tile_barrier<0>();
     if (kt + kAttBufs - 1 < nkt) {
       const int b = (kt + kAttBufs - 1) % kAttBufs;
       stage_k_tile(Kh, kt + kAttBufs - 1, lds[b][0], wave, lane);
