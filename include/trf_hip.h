@@ -18,9 +18,11 @@
  *
  * Sequence buffers (written by trf_qkv_rope_gemm, read by trf_attention), bf16, with
  * Lpad = trf_seq_pad(L) and sequence s, head h, position p, head feature d:
- *     Q  [nseq][8][Lpad][64]   index ((s*8 + h)*Lpad + p)*64 + d   (rotated, times log2(e))
- *     K  [nseq][8][Lpad][64]   same index                         (rotated)
- *     Vt [nseq][8][64][Lpad]   index ((s*8 + h)*64 + d)*Lpad + p   (transposed V)
+ *     Q  [nseq][8][8][Lpad][8]  index (((s*8 + h)*8 + d/8)*Lpad + p)*8 + d%8  (rotated, times log2(e))
+ *     K  [nseq][8][8][Lpad][8]  same index                                   (rotated)
+ *     Vt [nseq][8][64][Lpad]    index ((s*8 + h)*64 + d)*Lpad + p             (transposed V)
+ * Q and K are chunk-major: the 16-byte chunk of features 8c..8c+7 of consecutive positions is
+ * contiguous, which is how the MFMA accumulators of the projection hold them.
  * Positions p >= L are written as zeros.  G is fp32 [ntok][8] = sigmoid(gate logits).
  *
  * All bf16 values are passed as uint16_t bit patterns.  Error codes: 0 = ok; otherwise

@@ -3,7 +3,7 @@
 Each function reproduces where the reference kernels (src/turbo_roformer/csrc/kernels.cpp) round to
 bf16 and what they keep in fp32, with fp64 accumulation, so that a correct device kernel differs from
 it only by fp32 summation order (occasionally one bf16 step at a rounding boundary).  Inputs and outputs
-use the sequence-buffer layouts of include/trf_hip.h: Q, K [nseq, 8, Lpad, 64], Vt [nseq, 8, 64, Lpad]
+use the sequence-buffer layouts of include/trf_hip.h: Q, K chunk-major [nseq, 8, 8, Lpad, 8], Vt [nseq, 8, 64, Lpad]
 bf16, G [ntok, 8] fp32, tokens in (chunk, frame, band) order.
 """
 
@@ -43,6 +43,18 @@ def add_rmsnorm(X: Tensor, Y: Tensor | None, out_dtype=torch.bfloat16) -> tuple[
     return Xn, out
 
 
+def qk_chunk_major(X: Tensor) -> Tensor:
+    """[nseq, H, Lpad, 64] -> the device's chunk-major [nseq, H, 8, Lpad, 8] (trf_hip.h)."""
+    nseq, h, lp, d = X.shape
+    return X.view(nseq, h, lp, d // 8, 8).permute(0, 1, 3, 2, 4).contiguous()
+
+
+def qk_rows(X: Tensor) -> Tensor:
+    """Chunk-major [nseq, H, 8, Lpad, 8] -> rows [nseq, H, Lpad, 64]."""
+    nseq, h, c, lp, e = X.shape
+    return X.permute(0, 1, 3, 2, 4).reshape(nseq, h, lp, c * e)
+
+
 def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, batch: int, T: int, F: int):
     """qkv_rope_gemm (kernels.cpp:439-540): fp32 accumulators, fp32 rotary of q and k, bf16 outputs,
     fp32 sigmoid gates.  Returns Q, K, Vt (padded, zero pads) and G.
@@ -71,7 +83,7 @@ def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, ba
     Q[:, :, :L] = q
     K[:, :, :L] = k
     Vt[:, :, :, :L] = v.transpose(-1, -2)
-    return Q, K, Vt, g
+    return qk_chunk_major(Q), qk_chunk_major(K), Vt, g
 
 
 def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int, T: int, F: int,
@@ -81,6 +93,7 @@ def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int
     bf16, token order."""
     idx = token_index(mode, batch, T, F)
     nseq, L = idx.shape
+    Q, K = qk_rows(Q), qk_rows(K)
     O = torch.empty(batch * T * F, H * DH, dtype=torch.bfloat16)
     for s0 in range(0, nseq, chunk):
         s1 = min(nseq, s0 + chunk)

@@ -96,7 +96,7 @@ def test_qkv_rope_gemm(hip, layers, mode, batch, T, F):
     assert_bf16_close(Kr, K, "K")
     assert_bf16_close(Vr, Vt, "Vt")
     torch.testing.assert_close(G.cpu(), Gr, rtol=2e-5, atol=2e-6)
-    assert (Q.cpu()[:, :, L:] == 0).all() and (K.cpu()[:, :, L:] == 0).all() and (Vt.cpu()[..., L:] == 0).all()
+    assert (Q.cpu()[:, :, :, L:] == 0).all() and (K.cpu()[:, :, :, L:] == 0).all() and (Vt.cpu()[..., L:] == 0).all()
 
 
 ATT_SHAPES = QKV_SHAPES + [(0, 1, 1700, 2), (0, 1, 200, 9), (1, 3, 11, 64)]
@@ -121,7 +121,7 @@ def test_attention(hip, layers, mode, batch, T, F):
     # Q carries log2(e), so the natural-log scores are q.k * ln 2.
     L = T if mode == 0 else F
     idx = ok.token_index(mode, batch, T, F)
-    q, k = Q[:, :, :L].double(), K[:, :, :L].double()
+    q, k = ok.qk_rows(Q)[:, :, :L].double(), ok.qk_rows(K)[:, :, :L].double()
     v = Vt[:, :, :, :L].double().transpose(-1, -2)
     o = torch.softmax((q @ k.transpose(-1, -2)) * math.log(2.0), dim=-1) @ v
     o = o * G[idx].permute(0, 2, 1).unsqueeze(-1).double()

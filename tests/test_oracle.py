@@ -136,7 +136,7 @@ def test_emulated_attention_rows_and_gate():
     for j in range(5):
         Vt[:, :, j, j] = 1.0
     G = torch.rand(5, 8, generator=g)
-    O = ok.attention(Q, K, Vt, G, 0, batch, T, F_).float().view(5, 8, 64)
+    O = ok.attention(ok.qk_chunk_major(Q), ok.qk_chunk_major(K), Vt, G, 0, batch, T, F_).float().view(5, 8, 64)
     # Q carries log2(e): the natural-log scores are q.k * ln 2
     p = torch.softmax(Q[0, :, :5].double() @ K[0, :, :5].double().transpose(-1, -2) * math.log(2.0), -1)
     torch.testing.assert_close(O[:, :, :5], (p * G.t().double()[:, :, None]).permute(1, 0, 2).float(), rtol=1e-2, atol=2e-3)
@@ -150,8 +150,12 @@ def test_kernel_emulation_pads_and_layouts():
     xn = torch.randn(n, 256, generator=g).to(torch.bfloat16)
     W = (0.05 * torch.randn(1544, 256, generator=g)).to(torch.bfloat16)
     Q, K, Vt, G = ok.qkv_rope(xn, W, torch.zeros(8), weights.rotary_freqs(), 1, 2, T, F_)
-    assert Q.shape == (6, 8, 128, 64) and Vt.shape == (6, 8, 64, 128)
-    assert (Q[:, :, 70:] == 0).all() and (Vt[..., 70:] == 0).all()
+    assert Q.shape == (6, 8, 8, 128, 8) and Vt.shape == (6, 8, 64, 128)
+    assert (Q[:, :, :, 70:] == 0).all() and (Vt[..., 70:] == 0).all()
+    # chunk-major: element (((s*8 + h)*8 + d/8)*Lpad + p)*8 + d%8 holds feature d of position p
+    rows = ok.qk_rows(Q)
+    assert torch.equal(Q.flatten()[((5 * 8 + 3) * 8 + 2) * 128 * 8 + 9 * 8 + 5], rows[5, 3, 9, 21])
+    assert torch.equal(ok.qk_chunk_major(rows), Q)
     # V of token (c=1, t=2, f=5) lands in sequence c*T+t = 5 at position 5, transposed, un-rotated
     tok = (1 * T + 2) * F_ + 5
     v = (xn[tok].double() @ W[1024:1536].double().t()).float().to(torch.bfloat16).view(8, 64)

@@ -288,10 +288,12 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
 #pragma unroll
       for (int tt = 0; tt < kQkvTps; ++tt) {
         const int t = kQkvTps * stage + tt, h = (t & 15) >> 1, half = tt & 1;
-        uint16_t* dst = base + ((int64_t(s) * kHeads + h) * Lpad + p) * kHeadDim;
+        // chunk-major rows: features 8c..8c+7 of position p at ((s*8 + h)*8 + c)*Lpad + p, so the
+        // 32 lanes of a half-wave store 32 consecutive 16-byte chunks (hh fills bytes 8hh..8hh+7)
+        uint16_t* dst = base + ((int64_t(s) * kHeads + h) * 8 * Lpad + p) * 8 + 4 * hh;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int d0 = 32 * half + row_of_group(g, hh);
+          const int c8 = __builtin_amdgcn_readfirstlane((4 * half + g) * Lpad * 8);  // chunk 4 half + g
           const float2 c = rc[half][g], sn = rsn[half][g];
           const float a0 = acc[tt][4 * g], a1 = acc[tt][4 * g + 1], a2 = acc[tt][4 * g + 2], a3 = acc[tt][4 * g + 3];
           u32x2 o = {0u, 0u};
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
             o[0] = pk_bf16(fmaf(a0, c.x, -(a1 * sn.x)) * sc, fmaf(a1, c.x, a0 * sn.x) * sc);
             o[1] = pk_bf16(fmaf(a2, c.y, -(a3 * sn.y)) * sc, fmaf(a3, c.y, a2 * sn.y) * sc);
           }
-          *reinterpret_cast<u32x2*>(dst + d0) = o;
+          *reinterpret_cast<u32x2*>(dst + c8) = o;
         }
       }
     } else {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
@@ -417,21 +419,22 @@ constexpr int kAttBlockQ = kAttWaves * 32 * kAttQT;  // queries per workgroup
 // pattern is conflict-free for every group of 16 lanes (and for groups of 8 with 32 banks).
 __device__ __forceinline__ int chunk_swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
 
-// This wave's share of staging one 8 KB tile (64 rows x 8 chunks of 16 B) into LDS: rows 16w..16w+15
-// (two instructions of 8 rows).  Row R of the K tile holds key (R&32)|pi(R&31); row R of the V^T tile
-// holds head feature R.
-__device__ __forceinline__ void stage_k_tile(const uint16_t* __restrict__ Kh, int kt, u32x4* lds_tile, int wave,
-                                             int lane) {
+// This wave's share of staging one 8 KB K tile into LDS, chunk-major like K itself: LDS block c
+// (64 rows x 16 B) holds features 8c..8c+7 of the tile's 64 keys, row R = key (R&32)|pi(R&31).  Wave w
+// stages chunks 2w and 2w+1, one 1 KB instruction each (64 consecutive rows of one chunk plane).
+__device__ __forceinline__ void stage_k_tile(const uint16_t* __restrict__ Kh, int kt, int Lpad, u32x4* lds_tile,
+                                             int wave, int lane) {
+  const int key = (lane & 32) | key_perm(lane & 31);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int R = 16 * wave + 8 * i + (lane >> 3), pc = lane & 7;
-    const int key = (R & 32) | key_perm(R & 31);
-    const uint16_t* src = Kh + int64_t(kt * 64 + key) * kHeadDim + 8 * (pc ^ chunk_swz(R));
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src), lds_tile + (16 * wave + 8 * i) * 8, 16,
-                                     0, 0);
+    const int c = 2 * wave + i;
+    const uint16_t* src = Kh + (int64_t(c) * Lpad + kt * 64 + key) * 8;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src), lds_tile + c * 64, 16, 0, 0);
   }
 }
 
+// This wave's share of staging one 8 KB V^T tile (64 rows x 8 chunks of 16 B) into LDS: rows
+// 16w..16w+15 (two instructions of 8 rows).  Row R holds head feature R.
 __device__ __forceinline__ void stage_v_tile(const uint16_t* __restrict__ Vh, int kt, int Lpad, u32x4* lds_tile,
                                              int wave, int lane) {
 #pragma unroll
@@ -443,11 +446,11 @@ __device__ __forceinline__ void stage_v_tile(const uint16_t* __restrict__ Vh, in
   }
 }
 
-// K operands of one 32-key half of a tile.
+// K operands of one 32-key half of a tile (chunk 2ks+hh of rows 32kh..32kh+31: 16 lanes read 256
+// consecutive bytes, so the chunk-major tile needs no swizzle).
 __device__ __forceinline__ void load_k_half(const u32x4* __restrict__ Kl, int kh, int j, int hh, u32x4 (&ka)[4]) {
-  const int R = 32 * kh + j;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) ka[ks] = Kl[R * 8 + ((2 * ks + hh) ^ chunk_swz(R))];
+  for (int ks = 0; ks < 4; ++ks) ka[ks] = Kl[(2 * ks + hh) * 64 + 32 * kh + j];
 }
 
 // Pass-1 work of one 64-key tile: scores for both query tiles, running max.
@@ -544,7 +547,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
     const int q = q0 + 32 * qt + j;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      qb[qt][ks] = q < Lpad ? reinterpret_cast<const u32x4*>(Qh + int64_t(q) * kHeadDim)[2 * ks + hh] : zero4();
+      qb[qt][ks] = q < Lpad ? *reinterpret_cast<const u32x4*>(Qh + (int64_t(2 * ks + hh) * Lpad + q) * 8) : zero4();
   }
 
   const int nkt = Lpad / 64;
@@ -554,13 +557,13 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   for (int qt = 0; qt < kAttQT; ++qt) m[qt] = -INFINITY;
 #pragma unroll
   for (int i = 0; i < kAttBufs - 1; ++i)
-    if (i < nkt) stage_k_tile(Kh, i, lds[i][0], wave, lane);
+    if (i < nkt) stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
   for (int kt = 0; kt < nkt; ++kt) {
     if (kt + kAttBufs - 2 < nkt)  // the younger tiles kt+1 .. kt+kAttBufs-2 are in flight: 2 loads each
       tile_barrier<2 * (kAttBufs - 2)>();
     else
       tile_barrier<0>();
-    if (kt + kAttBufs - 1 < nkt) stage_k_tile(Kh, kt + kAttBufs - 1, lds[(kt + kAttBufs - 1) % kAttBufs][0], wave, lane);
+    if (kt + kAttBufs - 1 < nkt) stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[(kt + kAttBufs - 1) % kAttBufs][0], wave, lane);
     if (!active) continue;
     if (kt + 1 < nkt)
       attn_max_tile<false>(lds[kt % kAttBufs][0], qb, 0, L, j, hh, m);
@@ -585,7 +588,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
 #pragma unroll
   for (int i = 0; i < kAttBufs - 1; ++i)
     if (i < nkt) {
-      stage_k_tile(Kh, i, lds[i][0], wave, lane);
+      stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
       stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
     }
   for (int kt = 0; kt < nkt - 1; ++kt) {
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
       tile_barrier<0>();
     if (kt + kAttBufs - 1 < nkt) {
       const int b = (kt + kAttBufs - 1) % kAttBufs;
-      stage_k_tile(Kh, kt + kAttBufs - 1, lds[b][0], wave, lane);
+      stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[b][0], wave, lane);
       stage_v_tile(Vh, kt + kAttBufs - 1, Lpad, lds[b][1], wave, lane);
     }
     if (active) attn_pv_tile<false>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negm, lsum, o);
@@ -631,7 +634,7 @@ __global__ __launch_bounds__(256) void k_attn_short(const uint16_t* __restrict__
   for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      ka[kh][ks] = reinterpret_cast<const u32x4*>(Kh + int64_t(32 * kh + key_perm(j)) * kHeadDim)[2 * ks + hh];
+      ka[kh][ks] = *reinterpret_cast<const u32x4*>(Kh + (int64_t(2 * ks + hh) * Lp + 32 * kh + key_perm(j)) * 8);
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -644,7 +647,7 @@ __global__ __launch_bounds__(256) void k_attn_short(const uint16_t* __restrict__
     if (32 * qt >= L) break;
     u32x4 qb[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qb[ks] = reinterpret_cast<const u32x4*>(Qh + int64_t(q) * kHeadDim)[2 * ks + hh];
+    for (int ks = 0; ks < 4; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(Qh + (int64_t(2 * ks + hh) * Lp + q) * 8);
     f32x16 sacc[2];
     float m = -INFINITY;
 #pragma unroll

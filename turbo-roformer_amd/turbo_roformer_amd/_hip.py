@@ -236,10 +236,15 @@ def add_rmsnorm(X: torch.Tensor, Y: torch.Tensor | None, out: torch.Tensor, eps:
     _check(lib.trf_add_rmsnorm(X.data_ptr(), _ptr(Y), ydt, out.data_ptr(), odt, X.shape[0], eps, _stream()))
 
 
+def qk_shape(nseq: int, Lp: int) -> tuple[int, ...]:
+    """Chunk-major Q/K: [nseq, 8 heads, 8 chunks of 8 features, Lpad, 8] (trf_hip.h)."""
+    return (nseq, HEADS, HEAD_DIM // 8, Lp, 8)
+
+
 def seq_buffers(mode: int, batch: int, T: int, F: int, device="cuda") -> tuple[torch.Tensor, ...]:
-    """Q, K [nseq, 8, Lpad, 64] and Vt [nseq, 8, 64, Lpad] bf16, plus G [ntok, 8] fp32."""
+    """Q, K [nseq, 8, 8, Lpad, 8] (chunk-major) and Vt [nseq, 8, 64, Lpad] bf16, plus G [ntok, 8] fp32."""
     nseq, L, Lp = seq_shape(mode, batch, T, F)
-    Q = torch.empty(nseq, HEADS, Lp, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    Q = torch.empty(qk_shape(nseq, Lp), dtype=torch.bfloat16, device=device)
     K = torch.empty_like(Q)
     Vt = torch.empty(nseq, HEADS, HEAD_DIM, Lp, dtype=torch.bfloat16, device=device)
     G = torch.empty(batch * T * F, HEADS, dtype=torch.float32, device=device)
@@ -254,8 +259,8 @@ def qkv_rope_gemm(xn, layer, rope, mode, batch, T, F, Q, K, Vt, G) -> None:
     _need(xn, "xn", torch.bfloat16, (n, DIM))
     _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
     _need(rope, "rope", torch.float32, (2, L, HEAD_DIM // 2))
-    _need(Q, "Q", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
-    _need(K, "K", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
+    _need(Q, "Q", torch.bfloat16, qk_shape(nseq, Lp))
+    _need(K, "K", torch.bfloat16, qk_shape(nseq, Lp))
     _need(Vt, "Vt", torch.bfloat16, (nseq, HEADS, HEAD_DIM, Lp))
     _need(G, "G", torch.float32, (n, HEADS))
     _check(
@@ -271,8 +276,8 @@ def attention(Q, K, Vt, G, O, mode, batch, T, F) -> None:
     lib = load()
     nseq, L, Lp = seq_shape(mode, batch, T, F)
     n = batch * T * F
-    _need(Q, "Q", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
-    _need(K, "K", torch.bfloat16, (nseq, HEADS, Lp, HEAD_DIM))
+    _need(Q, "Q", torch.bfloat16, qk_shape(nseq, Lp))
+    _need(K, "K", torch.bfloat16, qk_shape(nseq, Lp))
     _need(Vt, "Vt", torch.bfloat16, (nseq, HEADS, HEAD_DIM, Lp))
     _need(G, "G", torch.float32, (n, HEADS))
     _need(O, "O", torch.bfloat16, (n, HEADS * HEAD_DIM))
