@@ -64,8 +64,12 @@ enum trf_dtype { TRF_F32 = 0, TRF_BF16 = 1 };
  *   lo = bf16(v - hi)) and compute hi.hi + hi.lo + lo.hi on the bf16 MFMA with fp32
  *   accumulation, which removes the four rounding points (W1, W2, xn, gelu(h)) that dominate the
  *   bf16 design's error.  It needs the lo weight parts (trf_layer_src.w_ff1_lo / w_ff2_lo).
- *   Attention, the QKV GEMM and the out-projection stay bf16 in both modes. */
-enum trf_precision { TRF_PREC_BF16 = 0, TRF_PREC_FF_SPLIT = 1 };
+ *   Attention, the QKV GEMM and the out-projection stay bf16 in every mode.
+ * TRF_PREC_FF_FP16: FF1 and FF2 take fp16 operands (xn, W1, gelu(h), W2: 11-bit significands
+ *   instead of bf16's 8) on the fp16 MFMA with fp32 accumulation, at the cost of the bf16 mode.  The
+ *   fp16 weights are fp16(w_ff* + w_ff*_lo), so the lo parts make them round from fp32.  Values
+ *   must stay within fp16 range (|x| < 65504), which holds for normalised inputs. */
+enum trf_precision { TRF_PREC_BF16 = 0, TRF_PREC_FF_SPLIT = 1, TRF_PREC_FF_FP16 = 2 };
 
 /* Same type as hipStream_t; NULL is the default stream. */
 typedef struct ihipStream_t* trf_stream_t;

@@ -153,6 +153,17 @@ def ff_split(X: Tensor, W1: Tensor, b1: Tensor, W2: Tensor, b2: Tensor) -> tuple
     return y, (y.double() / y.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).to(torch.bfloat16)
 
 
+def ff_fp16(X: Tensor, W1: Tensor, b1: Tensor, W2: Tensor, b2: Tensor) -> tuple[Tensor, Tensor]:
+    """The feed-forward sub-layer in the library's fp16 precision (TRF_PREC_FF_FP16): xn = X/|X| in fp32,
+    then xn, W1, gelu(h) and W2 rounded to fp16 (round to nearest even) with fp64 sums here; returns the
+    fp32 residual stream and the bf16 xn of the result.  Not a reference kernel: the library's own mode."""
+    xn = (X.double() / X.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).float()
+    h = (xn.half().double() @ W1.float().half().double().t()).float() + b1.float()
+    g = (0.5 * h.double() * (1.0 + torch.erf(h.double() / math.sqrt(2.0)))).float()
+    y = X.float() + (g.half().double() @ W2.float().half().double().t()).float() + b2.float()
+    return y, (y.double() / y.double().norm(dim=-1, keepdim=True).clamp_min(1e-12)).to(torch.bfloat16)
+
+
 def bf16_weights(P: dict) -> dict:
     """bf16 operands of one folded sub-layer (oracle.folded.fold output), as the kernels see them."""
     return dict(
@@ -166,7 +177,7 @@ def bf16_weights(P: dict) -> dict:
 def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int, precision: str = "bf16") -> Tensor:
     """The fused-op sequence of ``_transformer_cpp`` (fast.py:269-341) with bf16 rounding at the same
     points as the reference kernels; X is [batch*T*F, 256] fp32, returns a new tensor.
-    ``precision="ff_split"`` replaces the feed-forward by ``ff_split``."""
+    ``precision="ff_split"`` / ``"ff_fp16"`` replaces the feed-forward by ``ff_split`` / ``ff_fp16``."""
     X = X.float().clone()
     _, xn = add_rmsnorm(X, None)
     for P in layers:
@@ -174,8 +185,8 @@ def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int, precision: 
         Q, K, Vt, G = qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], w["mode"], batch, T, F)
         O = attention(Q, K, Vt, G, w["mode"], batch, T, F)
         X, xn = gemm_res_norm(O, w["Wo"], None, X)
-        if precision == "ff_split":
-            X, xn = ff_split(X, P["W1"], P["b1"], P["W2"], P["b2"])
+        if precision in ("ff_split", "ff_fp16"):
+            X, xn = (ff_split if precision == "ff_split" else ff_fp16)(X, P["W1"], P["b1"], P["W2"], P["b2"])
             continue
         Hh = gemm_gelu(xn, w["W1"], w["b1"])
         X, xn = gemm_res_norm(Hh, w["W2"], w["b2"], X)

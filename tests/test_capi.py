@@ -28,8 +28,8 @@ def test_version_and_sizes(lib):
     assert [lib.trf_seq_pad(L) for L in (1, 62, 64, 65, 1700, 1701)] == [64, 64, 64, 128, 1728, 1728]
     assert lib.trf_layer_packed_bytes() % 256 == 0
     # bf16 W_qkvg (49 tiles of 32 rows), W_out, W1, W2 in 32x32 tiles, W_out and the hi and lo parts of
-    # W1 and W2 in 16x16 tiles, and the biases
-    assert lib.trf_layer_packed_bytes() == (49 * 32 * 256 + 2 * 256 * 512 + 6 * 1024 * 256) * 2 + 256 + (1024 + 256) * 4
+    # W1 and W2 in 16x16 tiles, fp16 W1 and W2 in 32x32 tiles, and the biases
+    assert lib.trf_layer_packed_bytes() == (49 * 32 * 256 + 2 * 256 * 512 + 8 * 1024 * 256) * 2 + 256 + (1024 + 256) * 4
     # Q/K/Vt elements: time 62 bands x 8 heads x 1728 x 64; freq 1701 frames x 8 x 64 x 64
     assert lib.trf_seq_buffer_elems(0, 1, 1701, 62) == 62 * 8 * 1728 * 64
     assert lib.trf_seq_buffer_elems(1, 1, 1701, 62) == 1701 * 8 * 64 * 64
@@ -54,7 +54,7 @@ def test_argument_errors_need_no_device(lib):
     assert b"workspace" in lib.trf_last_error()
     assert lib.trf_stack_forward(p, 1, 8, 2, None, None, 0, 7, None, None, p, 1 << 30, None) == 1
     assert b"precision" in lib.trf_last_error()
-    assert lib.trf_ff_block(p, 1, 8, 2, p, 2, p, 1 << 30, None) == 1
+    assert lib.trf_ff_block(p, 1, 8, 2, p, 3, p, 1 << 30, None) == 1
     assert b"precision" in lib.trf_last_error()
     assert lib.trf_seq_buffer_elems(2, 1, 8, 2) == -1
     assert lib.trf_stack_workspace_bytes(0, 8, 2) == 0

@@ -36,7 +36,7 @@ def x_bf16():
     return torch.randn(T, F, 256, generator=g).to(torch.bfloat16)
 
 
-@pytest.fixture(scope="module", params=["ff_split", "bf16"])
+@pytest.fixture(scope="module", params=["ff_fp16", "ff_split", "bf16"])
 def stack(request, hip, sd):
     return HipStack(sd, DEV, precision=request.param)
 
@@ -103,6 +103,8 @@ def test_feed_forward_block_full_shape(stack, sd, x_bf16):
     P = folded.fold(sd, 1)[0]
     if stack.precision == "ff_split":
         y, _ = ok.ff_split(xs, P["W1"], P["b1"], P["W2"], P["b2"])
+    elif stack.precision == "ff_fp16":
+        y, _ = ok.ff_fp16(xs, P["W1"], P["b1"], P["W2"], P["b2"])
     else:
         w = ok.bf16_weights(P)
         _, xn = ok.add_rmsnorm(xs, None)
@@ -114,6 +116,8 @@ def test_feed_forward_block_full_shape(stack, sd, x_bf16):
     if stack.precision == "ff_split":
         # split operands: ~2^-16 relative products; the remaining error is the fp32 GELU (A&S 7.1.26)
         assert s_ref >= 90.0
+    elif stack.precision == "ff_fp16":
+        assert s_ref >= s_design - 1.0 and s_design >= 65.0  # fp16 operands: ~18 dB above bf16
     else:
         assert s_ref >= s_design - 1.0
     assert s_emu >= 50.0

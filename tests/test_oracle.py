@@ -192,3 +192,20 @@ def test_ff_split_matches_fp32_feed_forward(tiny_sd):
     y, xn = ok.ff_split(x, P["W1"], P["b1"], P["W2"], P["b2"])
     assert snr_db(ref.numpy(), y.double().numpy()) >= 90.0
     assert torch.equal(xn, (y.double() / y.double().norm(dim=-1, keepdim=True)).to(torch.bfloat16))
+
+
+def test_ff_fp16_between_bf16_and_fp32(tiny_sd):
+    """fp16 operands (11-bit significands) sit between the bf16 design and fp32: ~18 dB above bf16."""
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(300, 256, generator=g)
+    prefix = "layers.0.0.layers.0.1"
+    ref = reference.feed_forward(x.double(), {k: v.double() for k, v in tiny_sd.items()}, prefix) + x.double()
+    P = folded.fold(tiny_sd, CFG["depth"])[0]
+    y16, _ = ok.ff_fp16(x, P["W1"], P["b1"], P["W2"], P["b2"])
+    w = ok.bf16_weights(P)
+    _, xn = ok.add_rmsnorm(x, None)
+    yb, _ = ok.gemm_res_norm(ok.gemm_gelu(xn, w["W1"], w["b1"]), w["W2"], w["b2"], x)
+    d16 = snr_db((ref - x.double()).numpy(), (y16.double() - x.double()).numpy())
+    db = snr_db((ref - x.double()).numpy(), (yb.double() - x.double()).numpy())
+    assert d16 >= db + 12.0, (d16, db)
+    assert d16 >= 60.0

@@ -39,8 +39,8 @@ int check_shape(int32_t batch, int32_t T, int32_t F) {
 }
 
 int check_precision(int32_t precision) {
-  if (precision != TRF_PREC_BF16 && precision != TRF_PREC_FF_SPLIT)
-    return fail(TRF_ERR_ARG, "precision must be 0 (bf16) or 1 (ff split), got %d", precision);
+  if (precision != TRF_PREC_BF16 && precision != TRF_PREC_FF_SPLIT && precision != TRF_PREC_FF_FP16)
+    return fail(TRF_ERR_ARG, "precision must be 0 (bf16), 1 (ff split) or 2 (ff fp16), got %d", precision);
   return TRF_OK;
 }
 
@@ -117,7 +117,7 @@ struct Events {
 // One sub-layer on an already normalised xn: qkv + rotary, attention, then the fused out-proj +
 // residual + norm, and (with_ff) FF1 + GELU + FF2 + residual + norm in the same kernel.
 int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
-              int64_t n, bool with_ff, bool split_ff, hipStream_t st, const Events& ev = Events{}) {
+              int64_t n, bool with_ff, int ff_precision, hipStream_t st, const Events& ev = Events{}) {
   TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
   trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
   TRF_TRY(check_launch("qkv_rope_gemm"));
@@ -127,7 +127,7 @@ int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const flo
   TRF_TRY(check_launch("attention"));
   TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
   TRF_TRY(ev.record(TRF_SLOT_POST, 0, st));
-  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, split_ff, 1e-12f, st);
+  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, ff_precision, 1e-12f, st);
   TRF_TRY(check_launch("post_attention"));
   return ev.record(TRF_SLOT_POST, 1, st);
 }
@@ -161,8 +161,8 @@ int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const*
     Events ev;
     ev.ev = n_events ? events : nullptr;
     ev.layer = i;
-    TRF_TRY(run_layer(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, true,
-                      precision == TRF_PREC_FF_SPLIT, st, ev));
+    TRF_TRY(run_layer(X, sh, layer, modes[i] == TRF_MODE_TIME ? rope_time : rope_freq, w, n, true, precision,
+                      st, ev));
   }
   return TRF_OK;
 }
@@ -209,6 +209,9 @@ int trf_pack_layer(const trf_layer_src* src, void* dst, trf_stream_t stream) {
   trf::launch_pack(src->w_ff1_lo, trf::kHidden, trf::kDim, trf::kPack16RegOrder, d + trf::kOffFf1Lo16, st);
   trf::launch_pack(src->w_ff2, trf::kDim, trf::kHidden, trf::kPack16RegOrder, d + trf::kOffFf2Hi16, st);
   trf::launch_pack(src->w_ff2_lo, trf::kDim, trf::kHidden, trf::kPack16RegOrder, d + trf::kOffFf2Lo16, st);
+  // operands of the fp16 feed-forward: fp16(hi + lo)
+  trf::launch_pack_f16(src->w_ff1, src->w_ff1_lo, trf::kHidden, trf::kDim, d + trf::kOffFf1F16, st);
+  trf::launch_pack_f16(src->w_ff2, src->w_ff2_lo, trf::kDim, trf::kHidden, d + trf::kOffFf2F16, st);
   return check_launch("pack_layer");
 }
 
@@ -314,7 +317,7 @@ int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pa
   trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
   if (int rc = check_launch("add_rmsnorm")) return rc;
   return run_layer(X, trf::seq_shape(mode, batch, T, F), static_cast<const uint8_t*>(packed_layer), rope, w, n,
-                   false, false, st);
+                   false, TRF_PREC_BF16, st);
 }
 
 int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer, int32_t precision,
@@ -331,7 +334,7 @@ int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pack
   const int64_t n = int64_t(batch) * T * F;
   trf::launch_add_rmsnorm(X, nullptr, 0, w.xn, 1, n, 1e-12f, st);
   if (int rc = check_launch("add_rmsnorm")) return rc;
-  trf::launch_ff(static_cast<const uint8_t*>(packed_layer), X, w.xn, n, precision == TRF_PREC_FF_SPLIT, 1e-12f, st);
+  trf::launch_ff(static_cast<const uint8_t*>(packed_layer), X, w.xn, n, precision, 1e-12f, st);
   return check_launch("feed_forward");
 }
 

@@ -44,7 +44,13 @@ constexpr size_t kOffFf1Hi16 = kOffOut16 + kSzOut;
 constexpr size_t kOffFf1Lo16 = kOffFf1Hi16 + kSzFf1;
 constexpr size_t kOffFf2Hi16 = kOffFf1Lo16 + kSzFf1;
 constexpr size_t kOffFf2Lo16 = kOffFf2Hi16 + kSzFf2;
-constexpr size_t kLayerBytes = kOffFf2Lo16 + kSzFf2;
+// fp16 W1 and W2 (32x32 register order, fp16(hi + lo)) for the fp16 feed-forward.
+constexpr size_t kOffFf1F16 = kOffFf2Lo16 + kSzFf2;
+constexpr size_t kOffFf2F16 = kOffFf1F16 + kSzFf1;
+constexpr size_t kLayerBytes = kOffFf2F16 + kSzFf2;
+
+// Feed-forward arithmetic (the trf_precision values of trf_hip.h).
+enum FfPrecision { kFfBf16 = 0, kFfSplit = 1, kFfFp16 = 2 };
 
 // Operand tile layouts of launch_pack.
 enum PackLayout { kPack32Natural = 0, kPack32RegOrder = 1, kPack16Natural = 2, kPack16RegOrder = 3 };
@@ -67,6 +73,8 @@ inline SeqShape seq_shape(int mode, int batch, int T, int F) {
 // Kernel launchers (trf_kernels.hip).  They only enqueue work; the caller checks errors.
 // Pack W [rows][K] bf16 into MFMA A-operand tiles (layout: PackLayout); W == nullptr packs zeros.
 void launch_pack(const uint16_t* W, int rows, int K, int layout, uint8_t* dst, hipStream_t st);
+// fp16(hi + lo) operand tiles in 32x32 register order (lo may be null).
+void launch_pack_f16(const uint16_t* hi, const uint16_t* lo, int rows, int K, uint8_t* dst, hipStream_t st);
 void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st);
 void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n,
                         float eps, hipStream_t st);
@@ -77,12 +85,12 @@ void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, 
 void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
                           int64_t n, float eps, hipStream_t st);
 void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);
-// Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm].  split_ff selects
-// split-bf16 operands (hi + lo) for both FF GEMMs.
+// Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm]; ff_precision is a
+// FfPrecision value for the two FF GEMMs.
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
-                      bool split_ff, float eps, hipStream_t st);
-// Fused FF1 + GELU + FF2 + residual + norm on X (updated in place); xn is written as X / |X|.
-// The bf16 variant reads its FF1 input from xn, the split variant normalises X itself.
-void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool split_ff, float eps, hipStream_t st);
+                      int ff_precision, float eps, hipStream_t st);
+// Fused FF1 + GELU + FF2 + residual + norm on X (updated in place, its norm computed in the kernel);
+// xn is written as X / |X|.
+void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, int ff_precision, float eps, hipStream_t st);
 
 }  // namespace trf

@@ -35,6 +35,20 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16 mfma32h(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+// Two fp32 -> packed fp16 pair, round to nearest even.
+__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
+  f16x2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ uint16_t to_bf16(float x) {
   return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
@@ -110,6 +124,38 @@ void launch_pack(const uint16_t* W, int rows, int K, int layout, uint8_t* dst, h
   const int tr = t16 ? 16 : 32, kstep = t16 ? 32 : 16;
   const int64_t total = int64_t((rows + tr - 1) / tr) * (K / kstep) * 64;
   hipLaunchKernelGGL(k_pack, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, W, rows, K, layout,
+                     reinterpret_cast<u32x4*>(dst));
+}
+
+// fp16 operand tiles, 32x32 register order, from hi + lo bf16 parts of the fp32 weights (lo optional):
+// dst = fp16(hi + lo), round to nearest even.
+__global__ void k_pack_f16(const uint16_t* __restrict__ hi, const uint16_t* __restrict__ lo, int rows, int K,
+                           u32x4* __restrict__ dst) {
+  const int ksteps = K / 16;
+  const int64_t total = int64_t((rows + 31) / 32) * ksteps * 64;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int lane = int(i % 64);
+  const int ks = int((i / 64) % ksteps);
+  const int t = int(i / (64 * ksteps));
+  const int row = 32 * t + (lane & 31), hh = lane >> 5;
+  u32x4 v = zero4();
+  if (row < rows) {
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = 16 * ks + (e < 4 ? 4 * hh + e : 8 + 4 * hh + (e - 4));  // register order
+      const int64_t idx = int64_t(row) * K + k;
+      f[e] = bf16_to_f32(hi[idx]) + (lo ? bf16_to_f32(lo[idx]) : 0.0f);
+    }
+    v = u32x4{pk_f16(f[0], f[1]), pk_f16(f[2], f[3]), pk_f16(f[4], f[5]), pk_f16(f[6], f[7])};
+  }
+  dst[i] = v;
+}
+
+void launch_pack_f16(const uint16_t* hi, const uint16_t* lo, int rows, int K, uint8_t* dst, hipStream_t st) {
+  const int64_t total = int64_t((rows + 31) / 32) * (K / 16) * 64;
+  hipLaunchKernelGGL(k_pack_f16, dim3(unsigned((total + 255) / 256)), dim3(256), 0, st, hi, lo, rows, K,
                      reinterpret_cast<u32x4*>(dst));
 }
 
@@ -859,13 +905,25 @@ __device__ __forceinline__ void store_row(const f32x16 (&acc)[8], float inv, flo
     }
 }
 
-template <bool OUTPROJ, bool FF>
+// FF1 / FF2 operand packing and product for the two feed-forward arithmetics of k_mlp.
+template <bool F16>
+__device__ __forceinline__ uint32_t pk_ff(float lo, float hi) {
+  return F16 ? pk_f16(lo, hi) : pk_bf16(lo, hi);
+}
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma_ff(u32x4 a, u32x4 b, f32x16 c) {
+  return F16 ? mfma32h(a, b, c) : mfma32(a, b, c);
+}
+
+// F16: the two FF GEMMs take fp16 operands (xn, W1, gelu(h), W2; 11-bit significands instead of bf16's
+// 8) on v_mfma_f32_32x32x16_f16 with fp32 accumulation; the out-projection stays bf16.
+template <bool OUTPROJ, bool FF, bool F16>
 __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, const uint8_t* __restrict__ layer,
                                              float* __restrict__ X, uint16_t* __restrict__ xn, int64_t n, float eps) {
   __shared__ u32x4 lds[2][32 * 64];  // 2 stages x 32 operand blocks of 1 KB
   const u32x4* wo = reinterpret_cast<const u32x4*>(layer + kOffOut);
-  const u32x4* w1 = reinterpret_cast<const u32x4*>(layer + kOffFf1);
-  const u32x4* w2 = reinterpret_cast<const u32x4*>(layer + kOffFf2);
+  const u32x4* w1 = reinterpret_cast<const u32x4*>(layer + (F16 ? kOffFf1F16 : kOffFf1));
+  const u32x4* w2 = reinterpret_cast<const u32x4*>(layer + (F16 ? kOffFf2F16 : kOffFf2));
   const float* b1 = reinterpret_cast<const float*>(layer + kOffBff1);
   const float* b2 = reinterpret_cast<const float*>(layer + kOffBff2);
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -888,25 +946,6 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
       for (int r = 0; r < 4; ++r) acc[t][4 * g + r] = x[r];
     }
 
-  u32x4 xb[16];  // FF1 B operands (xn in register order)
-  auto add_b2 = [&]() {  // a few bias vectors at a time: the accumulators already fill most registers
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 32 * t + row_of_group(g, hh));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][4 * g + r] += b[r];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  if (!OUTPROJ) {
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) xb[ks] = load_b_regorder(nr, ks, hh);
-    add_b2();
-  }
-
   constexpr int s_begin = OUTPROJ ? 0 : kOutStages;
   constexpr int s_end = FF ? kOutStages + kFfStages : kOutStages;  // stages: W_out k-steps, then hidden tiles
   auto issue = [&](int s, int buf) {
@@ -925,16 +964,15 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
     }
   };
 
-  const uint16_t* orow = O + trow * 512;
-  u32x4 ob[4];
-  auto load_o = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ob[i] = reinterpret_cast<const u32x4*>(orow)[2 * (4 * s + i) + hh];
-  };
-  if (OUTPROJ) load_o(0);
   issue(s_begin, 0);
-
   if (OUTPROJ) {
+    const uint16_t* orow = O + trow * 512;
+    u32x4 ob[4];
+    auto load_o = [&](int s) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ob[i] = reinterpret_cast<const u32x4*>(orow)[2 * (4 * s + i) + hh];
+    };
+    load_o(0);
     for (int s = 0; s < kOutStages; ++s) {
       stage_barrier();
       if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
@@ -948,57 +986,66 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
         __builtin_amdgcn_sched_barrier(0);  // bound the LDS operands in flight (register budget)
       }
     }
-    const float inv = acc_inv_norm(acc, eps);
-    if (!FF) {
-      if (valid) store_row(acc, inv, xr, nr, hh);
-      return;
-    }
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-      const int t = ks >> 1, g0 = 2 * (ks & 1);
-      xb[ks] = u32x4{pk_bf16(acc[t][4 * g0] * inv, acc[t][4 * g0 + 1] * inv),
-                     pk_bf16(acc[t][4 * g0 + 2] * inv, acc[t][4 * g0 + 3] * inv),
-                     pk_bf16(acc[t][4 * g0 + 4] * inv, acc[t][4 * g0 + 5] * inv),
-                     pk_bf16(acc[t][4 * g0 + 6] * inv, acc[t][4 * g0 + 7] * inv)};
-    }
-    add_b2();
   }
-  if (FF) {
-    for (int s = kOutStages; s < s_end; ++s) {
-      stage_barrier();
-      if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
-      const u32x4* Ls = lds[s & 1];
-      const int ht = s - kOutStages;
-      f32x16 h = zero16();
-#pragma unroll
-      for (int kg = 0; kg < 4; ++kg) {
-#pragma unroll
-        for (int ks = 4 * kg; ks < 4 * kg + 4; ++ks) h = mfma32(Ls[ks * 64 + lane], xb[ks], h);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      u32x4 hb[2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        float v[8];
-#pragma unroll
-        for (int gg = 0; gg < 2; ++gg) {
-          const f32x4 bb = *reinterpret_cast<const f32x4*>(b1 + 32 * ht + row_of_group(2 * c + gg, hh));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) v[4 * gg + r] = gelu_erf(h[8 * c + 4 * gg + r] + bb[r]);
-        }
-        hb[c] = u32x4{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]), pk_bf16(v[6], v[7])};
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int ot = 0; ot < 8; ++ot) {
-        acc[ot] = mfma32(Ls[(16 + 2 * ot) * 64 + lane], hb[0], acc[ot]);
-        acc[ot] = mfma32(Ls[(17 + 2 * ot) * 64 + lane], hb[1], acc[ot]);
-        if (ot & 1) __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    const float inv = acc_inv_norm(acc, eps);
+  const float inv = acc_inv_norm(acc, eps);
+  if (!FF) {
     if (valid) store_row(acc, inv, xr, nr, hh);
+    return;
   }
+  u32x4 xb[16];  // FF1 B operands: xn = X / |X| in register order, bf16 or fp16
+#pragma unroll
+  for (int ks = 0; ks < 16; ++ks) {
+    const int t = ks >> 1, g0 = 2 * (ks & 1);
+    xb[ks] = u32x4{pk_ff<F16>(acc[t][4 * g0] * inv, acc[t][4 * g0 + 1] * inv),
+                   pk_ff<F16>(acc[t][4 * g0 + 2] * inv, acc[t][4 * g0 + 3] * inv),
+                   pk_ff<F16>(acc[t][4 * g0 + 4] * inv, acc[t][4 * g0 + 5] * inv),
+                   pk_ff<F16>(acc[t][4 * g0 + 6] * inv, acc[t][4 * g0 + 7] * inv)};
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {  // + b2, a few bias vectors at a time (the accumulators fill most registers)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 32 * t + row_of_group(g, hh));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][4 * g + r] += b[r];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int s = kOutStages; s < s_end; ++s) {
+    const int ht = s - kOutStages;
+    f32x4 bb[4];  // b1 of this hidden tile, loaded before the next stage is issued (see stage_barrier)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) bb[g] = *reinterpret_cast<const f32x4*>(b1 + 32 * ht + row_of_group(g, hh));
+    stage_barrier();
+    if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
+    const u32x4* Ls = lds[s & 1];
+    f32x16 h = zero16();
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) {
+#pragma unroll
+      for (int ks = 4 * kg; ks < 4 * kg + 4; ++ks) h = mfma_ff<F16>(Ls[ks * 64 + lane], xb[ks], h);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    u32x4 hb[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float v[8];
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[4 * gg + r] = gelu_erf(h[8 * c + 4 * gg + r] + bb[2 * c + gg][r]);
+      hb[c] = u32x4{pk_ff<F16>(v[0], v[1]), pk_ff<F16>(v[2], v[3]), pk_ff<F16>(v[4], v[5]), pk_ff<F16>(v[6], v[7])};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ot = 0; ot < 8; ++ot) {
+      acc[ot] = mfma_ff<F16>(Ls[(16 + 2 * ot) * 64 + lane], hb[0], acc[ot]);
+      acc[ot] = mfma_ff<F16>(Ls[(17 + 2 * ot) * 64 + lane], hb[1], acc[ot]);
+      if (ot & 1) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const float inv2 = acc_inv_norm(acc, eps);
+  if (valid) store_row(acc, inv2, xr, nr, hh);
 }
 
 // ============================================================ split-bf16 feed-forward
@@ -1206,29 +1253,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
-                      bool split_ff, float eps, hipStream_t st) {
-  if (with_ff && split_ff) {
+                      int ff_precision, float eps, hipStream_t st) {
+  if (with_ff && ff_precision == kFfSplit) {
     const unsigned blocks = unsigned((n + 16 * kX3Waves - 1) / (16 * kX3Waves));
     hipLaunchKernelGGL(k_mlp_x3<true>, dim3(blocks), dim3(64 * kX3Waves), 0, st, O, layer, X, xn, n, eps);
     return;
   }
   const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
-  if (with_ff)
-    hipLaunchKernelGGL((k_mlp<true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+  if (!with_ff)
+    hipLaunchKernelGGL((k_mlp<true, false, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+  else if (ff_precision == kFfFp16)
+    hipLaunchKernelGGL((k_mlp<true, true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
   else
-    hipLaunchKernelGGL((k_mlp<true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+    hipLaunchKernelGGL((k_mlp<true, true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
 }
 
-void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool split_ff, float eps, hipStream_t st) {
-  if (split_ff) {
+void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, int ff_precision, float eps, hipStream_t st) {
+  const uint16_t* none = nullptr;
+  if (ff_precision == kFfSplit) {
     const unsigned blocks = unsigned((n + 16 * kX3Waves - 1) / (16 * kX3Waves));
-    hipLaunchKernelGGL(k_mlp_x3<false>, dim3(blocks), dim3(64 * kX3Waves), 0, st,
-                       static_cast<const uint16_t*>(nullptr), layer, X, xn, n, eps);
+    hipLaunchKernelGGL(k_mlp_x3<false>, dim3(blocks), dim3(64 * kX3Waves), 0, st, none, layer, X, xn, n, eps);
     return;
   }
   const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
-  hipLaunchKernelGGL((k_mlp<false, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st,
-                     static_cast<const uint16_t*>(nullptr), layer, X, xn, n, eps);
+  if (ff_precision == kFfFp16)
+    hipLaunchKernelGGL((k_mlp<false, true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, none, layer, X, xn, n, eps);
+  else
+    hipLaunchKernelGGL((k_mlp<false, true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, none, layer, X, xn, n, eps);
 }
 
 }  // namespace trf

@@ -25,8 +25,8 @@ ABI_VERSION = 2
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
 MODE_TIME, MODE_FREQ = 0, 1
-PREC_BF16, PREC_FF_SPLIT = 0, 1
-PRECISIONS = {"bf16": PREC_BF16, "ff_split": PREC_FF_SPLIT}
+PREC_BF16, PREC_FF_SPLIT, PREC_FF_FP16 = 0, 1, 2
+PRECISIONS = {"bf16": PREC_BF16, "ff_split": PREC_FF_SPLIT, "ff_fp16": PREC_FF_FP16}
 _F32, _BF16 = 0, 1
 
 _lock = threading.Lock()
@@ -310,11 +310,11 @@ SLOTS = ("qkv_rope_gemm", "attention", "post_attention")  # trf_kernel_slot orde
 
 
 def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], rope_time, rope_freq, ws,
-                  events: list | None = None, precision: str = "bf16") -> None:
+                  events: list | None = None, precision: str = "ff_fp16") -> None:
     """The whole stack on X [batch*T*F, 256] fp32, in place (fast.py:269-341).
 
-    ``precision``: ``"bf16"`` (every GEMM operand bf16, the reference kernels' arithmetic) or
-    ``"ff_split"`` (split-bf16 operands in the two FF GEMMs).
+    ``precision``: ``"bf16"`` (every GEMM operand bf16, the reference kernels' arithmetic),
+    ``"ff_fp16"`` (fp16 operands in the two FF GEMMs) or ``"ff_split"`` (split-bf16 operands there).
 
     ``events``: optional list of 2*5*len(layers) ``torch.cuda.Event`` (or None) recorded before/after
     each kernel (slot order ``SLOTS``), for per-kernel timing on the launch stream."""
@@ -368,7 +368,7 @@ def attn_block(X, batch, T, F, layer, mode, rope, ws) -> None:
     _check(lib.trf_attn_block(X.data_ptr(), batch, T, F, layer.data_ptr(), mode, rope.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
 
 
-def ff_block(X, batch, T, F, layer, ws, precision: str = "bf16") -> None:
+def ff_block(X, batch, T, F, layer, ws, precision: str = "ff_fp16") -> None:
     """One feed-forward sub-layer X += ff(X) (model.py:142)."""
     lib = load()
     prec = precision_code(precision)

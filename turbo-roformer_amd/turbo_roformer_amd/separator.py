@@ -53,14 +53,14 @@ class Separator:
     """Instrumental separation of single-stem stereo BS-RoFormer models, stack on the GPU.
 
     ``state_dict``/``cfg``: the model's weights (reference key names) and hyper-parameters; ``dim_t``:
-    frames per chunk (chunk = hop * (dim_t - 1)); ``precision``: ``"ff_split"`` or ``"bf16"`` (see
+    frames per chunk (chunk = hop * (dim_t - 1)); ``precision``: ``"ff_fp16"``, ``"ff_split"`` or ``"bf16"`` (see
     ``HipStack``); ``batch_chunks``: chunks per batched stack forward (0 = the whole song at once).
     ``backend``: ``"hip"``, or ``"auto"`` which is the same here (both raise ``HipUnavailable`` when the
     kernels cannot run, like the reference's explicit ``backend="kernels"``, separator.py:147-149).
     """
 
     def __init__(self, state_dict: Mapping[str, torch.Tensor], cfg: Mapping[str, Any], dim_t: int,
-                 device: str | torch.device = "cuda", precision: str = "ff_split", backend: str = "auto",
+                 device: str | torch.device = "cuda", precision: str = "ff_fp16", backend: str = "auto",
                  batch_chunks: int = 0):
         if backend not in BACKENDS:
             raise ValueError(f"backend must be one of {BACKENDS}")

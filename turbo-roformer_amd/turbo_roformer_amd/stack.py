@@ -7,10 +7,11 @@ the fp32 rotary tables on the host exactly as ``_tables`` does (fast.py:193-201)
 through ``trf_stack_forward``.  Work buffers are allocated once per shape and reused, so one forward
 runs at a time per instance (the reference's instances have the same rule, fast.py:24).
 
-Precision: ``"bf16"`` rounds every GEMM operand to bf16, the arithmetic of the reference kernels.
-``"ff_split"`` (the default) gives the two feed-forward GEMMs split-bf16 operands (hi + lo parts), which
-takes the mask from ~48 dB to ~59 dB SNR against the fp32 forward on seeded random weights; everything
-else is identical.
+Precision (the feed-forward GEMMs only; attention, QKV and the out-projection are bf16 in every mode):
+``"bf16"`` rounds every GEMM operand to bf16, the arithmetic of the reference kernels (~48 dB mask SNR
+against the fp32 forward on seeded random weights).  ``"ff_fp16"`` (the default) gives the two FF GEMMs
+fp16 operands at the same speed (~58 dB).  ``"ff_split"`` gives them split-bf16 operands, three
+products each (~59 dB, slower).
 """
 
 from __future__ import annotations
@@ -74,7 +75,7 @@ class HipStack:
     """Folded, packed weights of the whole stack on one device, plus cached tables and workspace."""
 
     def __init__(self, state_dict: Mapping[str, torch.Tensor], device: str | torch.device = "cuda",
-                 precision: str = "ff_split"):
+                 precision: str = "ff_fp16"):
         _hip.load()
         _hip.precision_code(precision)
         self.precision = precision
@@ -86,7 +87,7 @@ class HipStack:
         self.packed = torch.empty(len(prefixes), nb, dtype=torch.uint8, device=self.device)
         for i, (prefix, _) in enumerate(prefixes):
             w = fold_sublayer(sd, prefix)
-            for k in ("w_ff1", "w_ff2"):  # bf16 residuals of the fp32 FF weights (the split operands' lo parts)
+            for k in ("w_ff1", "w_ff2"):  # bf16 residuals of the fp32 FF weights (split lo parts; fp16 = hi + lo)
                 w[k + "_lo"] = w[k] - w[k].to(torch.bfloat16).float()
             dev = {
                 k: (v.to(torch.bfloat16) if k.startswith("w_") else v).to(self.device).contiguous()
@@ -106,7 +107,7 @@ class HipStack:
         torch.cuda.synchronize(self.device)
 
     @classmethod
-    def from_model(cls, model: torch.nn.Module, device="cuda", precision: str = "ff_split") -> HipStack:
+    def from_model(cls, model: torch.nn.Module, device="cuda", precision: str = "ff_fp16") -> HipStack:
         """From a loaded reference ``BSRoformer`` module (or anything with the same state-dict keys)."""
         return cls(model.state_dict(), device, precision)
 
