@@ -854,31 +854,43 @@ void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int
 
 // ============================================================ fused post-attention block
 // out-projection + residual + norm, then FF1 + GELU + FF2 + residual + norm, for 32 tokens per wave
-// (8 waves per workgroup):
-//   acc  := X                                  (the residual stream, in the MFMA accumulators)
-//   acc  += O . Wout^T                         (8 stages of 4 k-steps)      -> X1, xn1 = X1/|X1|
-//   acc  += b2 ; for each of 32 hidden tiles:  h = xn1 . W1t^T + b1; acc += gelu(h) . W2t^T
-//   X := acc ; xn := acc / |acc|
+// (8 waves per workgroup, two per SIMD):
+//   acc  := O . Wout^T + X                     (8 stages of 4 k-steps; X joins one 32-row tile per stage)
+//   xn1  := acc / |acc|                        (FF1 B operands, in registers)
+//   for each of 32 hidden tiles u:  h = b1 + xn1 . W1t^T ; acc += gelu(h) . W2t^T
+//   acc  += b2 ; X := acc ; xn := acc / |acc|
 // xn1 and each GELU tile go from accumulator registers straight into B operands (W1, W2 are packed in
 // register order), so neither xn1 nor the 1024-wide hidden activation ever leaves the chip.
 // Replaces gemm_res_norm (out) + oneDNN FF1 + gemm_res_norm (FF2) (fast.py:311-331, kernels.cpp:542-642).
 constexpr int kMlpWaves = 8;
 constexpr int kOutStages = 8;                // 32 k-steps of W_out, 4 per stage
 constexpr int kFfStages = kHidden / 32;      // one 32-wide hidden tile per stage
+constexpr int kMlpPrefetch = 4;              // LDS operands read ahead of their MFMA
 
-// erf-GELU x * Phi(x), Phi(x) = 0.5 (1 + erf(x / sqrt 2)), with erfc(|z|) from Abramowitz & Stegun
-// 7.1.26 (|error of erf| <= 1.5e-7): erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-z^2),
-// t = 1 / (1 + 0.3275911 z).  Negative x use Phi = erfc/2 directly (no cancellation).
+// erf-GELU x Phi(x) = max(x, 0) - 0.5|x| erfc(|x|/sqrt 2), with erfc from Abramowitz & Stegun 7.1.26
+// (|error of erf| <= 1.5e-7): erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-z^2),
+// t = 1/(1 + p z), p = 0.3275911.  Written in y = |x| sqrt(log2(e)/2) it is
+//   0.5|x| erfc(|x|/sqrt 2) = y t P(t) 2^(-y^2),  t = 1/(1 + p' y),  p' = p / sqrt(log2 e),
+//   P(t) = k (a1 + a2 t + a3 t^2 + a4 t^3 + a5 t^4),  k = 0.5 / sqrt(log2(e)/2),
+// 11 VALU operations and two transcendentals; |GELU error| <= 2.2e-7 over the real line.  For x < 0 the
+// result is the small erfc term itself (no cancellation).
+constexpr float kGeluC = 0.84932180028801904f;   // sqrt(log2(e)/2)
+constexpr float kGeluP = 0.27273748087922250f;   // 0.3275911 / sqrt(log2 e)
+constexpr float kGeluA1 = 0.15001945782716460f;  // k * 0.254829592
+constexpr float kGeluA2 = -0.16748465416966950f; // k * -0.284496736
+constexpr float kGeluA3 = 0.83679339239730750f;  // k * 1.421413741
+constexpr float kGeluA4 = -0.85547788041423880f; // k * -1.453152027
+constexpr float kGeluA5 = 0.62485469502846850f;  // k * 1.061405429
+
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-  float p = fmaf(1.061405429f, t, -1.453152027f);
-  p = fmaf(p, t, 1.421413741f);
-  p = fmaf(p, t, -0.284496736f);
-  p = fmaf(p, t, 0.254829592f);
-  const float q = p * t * __builtin_amdgcn_exp2f(-(z * z) * kLog2e);  // erfc(|z|)
-  const float phi = x >= 0.f ? fmaf(-0.5f, q, 1.0f) : 0.5f * q;
-  return x * phi;
+  const float y = fabsf(x) * kGeluC;
+  const float t = __builtin_amdgcn_rcpf(fmaf(kGeluP, y, 1.0f));
+  float p = fmaf(kGeluA5, t, kGeluA4);
+  p = fmaf(p, t, kGeluA3);
+  p = fmaf(p, t, kGeluA2);
+  p = fmaf(p, t, kGeluA1);
+  const float e = __builtin_amdgcn_exp2f(-(y * y));
+  return fmaf(-(y * t) * p, e, fmaxf(x, 0.0f));
 }
 
 __device__ __forceinline__ float acc_inv_norm(const f32x16 (&acc)[8], float eps) {
@@ -906,6 +918,8 @@ __device__ __forceinline__ void store_row(const f32x16 (&acc)[8], float inv, flo
 }
 
 // FF1 / FF2 operand packing and product for the two feed-forward arithmetics of k_mlp.
+// F16: the two FF GEMMs take fp16 operands (xn, W1, gelu(h), W2; 11-bit significands instead of bf16's
+// 8) on v_mfma_f32_32x32x16_f16 with fp32 accumulation; the out-projection stays bf16.
 template <bool F16>
 __device__ __forceinline__ uint32_t pk_ff(float lo, float hi) {
   return F16 ? pk_f16(lo, hi) : pk_bf16(lo, hi);
@@ -915,17 +929,165 @@ __device__ __forceinline__ f32x16 mfma_ff(u32x4 a, u32x4 b, f32x16 c) {
   return F16 ? mfma32h(a, b, c) : mfma32(a, b, c);
 }
 
-// F16: the two FF GEMMs take fp16 operands (xn, W1, gelu(h), W2; 11-bit significands instead of bf16's
-// 8) on v_mfma_f32_32x32x16_f16 with fp32 accumulation; the out-projection stays bf16.
+// This wave's 4 of stage s's 32 operand blocks into LDS.  Stages 0..7: W_out k-steps 4s..4s+3 of the
+// 8 tiles.  Feed-forward stage u = s - 8 (0..32): blocks 0..15 are W1 tile u (k-steps 0..15; none for
+// u = 32), blocks 16..31 W2 k-steps 2(u-1), 2(u-1)+1 of the 8 output tiles (for u = 0 k-steps 0, 1:
+// finite values that meet zero B operands).  Nothing for s past the last stage.
+__device__ __forceinline__ void mlp_issue(int s, u32x4* dst, const u32x4* wo, const u32x4* w1, const u32x4* w2,
+                                          int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int b = wave * 4 + i;
+    const u32x4* src;
+    if (s < kOutStages) {
+      src = wo + (int64_t(b >> 2) * 32 + 4 * s + (b & 3)) * 64;  // W_out tile b/4, k-step 4s + b%4
+    } else {
+      const int u = s - kOutStages;
+      if (b < 16) {
+        if (u >= kFfStages) continue;
+        src = w1 + (int64_t(u) * 16 + b) * 64;  // W1 tile u, k-step b
+      } else {
+        if (u > kFfStages) continue;
+        src = w2 + (int64_t((b - 16) >> 1) * 64 + 2 * (u > 0 ? u - 1 : 0) + (b & 1)) * 64;  // W2 tile (b-16)/2
+      }
+    }
+    lds_load_block(src, dst + b * 64, lane);
+  }
+}
+
+// Operand block of MFMA i of a feed-forward stage.  MODE 0: FF1(u) and FF2(u-1) alternate (even i: FF1
+// k-step i/2, block i/2; odd i: FF2 step j = i/2 into output tile j%8 with hidden half j/8, block
+// 16 + 2(j%8) + j/8), so the FF1 accumulator chain has an independent MFMA between its links.
+// MODE 2: FF2 only (step j = i).
+template <int MODE>
+__device__ __forceinline__ constexpr int ff_block_of(int i) {
+  const int j = MODE == 2 ? i : i >> 1;
+  if (MODE == 0 && !(i & 1)) return i >> 1;
+  return 16 + 2 * (j % 8) + j / 8;
+}
+
+// gelu(h) as the two register-order B operands of FF2.
+template <bool F16>
+__device__ __forceinline__ void mlp_gelu(const f32x16& h, u32x4 (&hb)[2]) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float v[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) v[r] = gelu_erf(h[8 * c + r]);
+    hb[c] = u32x4{pk_ff<F16>(v[0], v[1]), pk_ff<F16>(v[2], v[3]), pk_ff<F16>(v[4], v[5]), pk_ff<F16>(v[6], v[7])};
+  }
+}
+
+// The MFMAs of one feed-forward stage, each A operand read from LDS kMlpPrefetch MFMAs ahead (the
+// sched barriers keep that order).  MODE 0: h := b1(u) + xn . W1(u)^T and acc += hb . W2(u-1)^T,
+// interleaved; MODE 2: only the latter.
+template <bool F16, int MODE>
+__device__ __forceinline__ void mlp_ff_block(const u32x4* Ls, const f32x4* b1s, const u32x4 (&xb)[16],
+                                             const u32x4 (&hb)[2], int u, int hh, int lane, f32x16& h,
+                                             f32x16 (&acc)[8]) {
+  constexpr int N = MODE == 0 ? 32 : 16;
+  constexpr int D = kMlpPrefetch;
+  if (MODE == 0) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 b = b1s[8 * u + 2 * g + hh];  // h starts at b1
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h[4 * g + r] = b[r];
+    }
+  }
+  u32x4 a[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) a[i] = Ls[ff_block_of<MODE>(i) * 64 + lane];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (MODE == 0 && !(i & 1)) {
+      h = mfma_ff<F16>(a[i % D], xb[i >> 1], h);
+    } else {
+      const int j = MODE == 2 ? i : i >> 1;
+      acc[j % 8] = mfma_ff<F16>(a[i % D], hb[j / 8], acc[j % 8]);
+    }
+    if (i + D < N) a[i % D] = Ls[ff_block_of<MODE>(i + D) * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// 32 out-projection MFMAs of one stage: MFMA i -> output tile i%8, k-step i/8 of the stage (block
+// 4(i%8) + i/8), operands read from LDS kMlpPrefetch ahead.
+__device__ __forceinline__ void mlp_out_block(const u32x4* Ls, const u32x4 (&cur)[4], int lane, f32x16 (&acc)[8]) {
+  constexpr int D = kMlpPrefetch;
+  u32x4 a[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) a[i] = Ls[(4 * (i % 8) + i / 8) * 64 + lane];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    acc[i % 8] = mfma32(a[i % D], cur[i / 8], acc[i % 8]);
+    if (i + D < 32) a[i % D] = Ls[(4 * ((i + D) % 8) + (i + D) / 8) * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Feed-forward stage u read from LDS buffer Lcur, the other buffer being Lnext (both compile-time
+// buffers, see mlp_ff_stages).
+template <bool F16>
+__device__ __forceinline__ void mlp_ff_stage(int u, u32x4* Lcur, u32x4* Lnext, f32x16 (&acc)[8],
+                                             const u32x4 (&xb)[16], const f32x4* b1s, const u32x4* wo,
+                                             const u32x4* w1, const u32x4* w2, int wave, int lane, int hh,
+                                             bool early, f32x16& h, u32x4 (&hb)[2]) {
+  const int s = kOutStages + u;
+  if (!early && u > 0) {
+    stage_barrier();
+    mlp_issue(s + 1, Lnext, wo, w1, w2, wave, lane);
+  }
+  mlp_ff_block<F16, 0>(Lcur, b1s, xb, hb, u, hh, lane, h, acc);
+  if (early) {
+    stage_barrier();
+    mlp_issue(s + 2, Lcur, wo, w1, w2, wave, lane);  // nothing past the last stage
+  }
+  mlp_gelu<F16>(h, hb);
+}
+
+// The 33 feed-forward stages.  Stage u holds W1 of hidden tile u and W2 of tile u-1, and every wave runs
+// FF2(u-1) interleaved with FF1(u), then GELU(u) (stage 0 multiplies its W2 blocks by hb = 0; stage 32 is
+// FF2(31) alone).  The waves differ only in where the stage barrier falls: before the MFMAs ("late"
+// waves) or between the MFMAs and GELU ("early" waves, plus one barrier up front, so both take 33).
+// Waves w and w + 4 of a workgroup share a SIMD (read from HW_ID on gfx950), so pairing early waves
+// 4..7 with late waves 0..3 puts the two waves of a SIMD in opposite phases, one's GELU beside the
+// other's MFMAs.  Stage u+2 is loaded into stage u's buffer only after barrier u+1, when both kinds of
+// wave are done with it.  Stages go in pairs so that each one's buffers are compile-time constants: the
+// compiler can then tell the operand reads from the direct-to-LDS loads into the other buffer, and does
+// not wait for those loads before reading.
+template <bool F16>
+__device__ __forceinline__ void mlp_ff_stages(f32x16 (&acc)[8], const u32x4 (&xb)[16], u32x4 (*lds)[32 * 64],
+                                              const f32x4* b1s, const u32x4* wo, const u32x4* w1,
+                                              const u32x4* w2, int wave, int lane, int hh) {
+  constexpr int s0 = kOutStages;
+  static_assert(s0 % 2 == 0 && kFfStages % 2 == 0, "stage pairs start on buffer 0");
+  const bool early = wave >= kMlpWaves / 2;
+  u32x4 hb[2] = {zero4(), zero4()};
+  f32x16 h = zero16();
+  stage_barrier();
+  mlp_issue(s0 + 1, lds[1], wo, w1, w2, wave, lane);
+#pragma clang loop unroll(disable)
+  for (int u = 0; u < kFfStages; u += 2) {
+    mlp_ff_stage<F16>(u, lds[0], lds[1], acc, xb, b1s, wo, w1, w2, wave, lane, hh, early, h, hb);
+    mlp_ff_stage<F16>(u + 1, lds[1], lds[0], acc, xb, b1s, wo, w1, w2, wave, lane, hh, early, h, hb);
+  }
+  if (!early) stage_barrier();
+  mlp_ff_block<F16, 2>(lds[0], b1s, xb, hb, kFfStages, hh, lane, h, acc);
+}
+
 template <bool OUTPROJ, bool FF, bool F16>
 __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, const uint8_t* __restrict__ layer,
                                              float* __restrict__ X, uint16_t* __restrict__ xn, int64_t n, float eps) {
-  __shared__ u32x4 lds[2][32 * 64];  // 2 stages x 32 operand blocks of 1 KB
+  // One LDS object: 2 stages x 32 operand blocks of 1 KB, then b1 (4 KB) and b2 (1 KB).  (With a second
+  // __shared__ object written by direct-to-LDS loads, the compiler waits for those loads before every
+  // operand read.)
+  __shared__ u32x4 smem[2 * 32 * 64 + (kHidden + kDim) / 4];
+  u32x4 (*lds)[32 * 64] = reinterpret_cast<u32x4 (*)[32 * 64]>(smem);
+  u32x4* bias = smem + 2 * 32 * 64;
   const u32x4* wo = reinterpret_cast<const u32x4*>(layer + kOffOut);
   const u32x4* w1 = reinterpret_cast<const u32x4*>(layer + (F16 ? kOffFf1F16 : kOffFf1));
   const u32x4* w2 = reinterpret_cast<const u32x4*>(layer + (F16 ? kOffFf2F16 : kOffFf2));
-  const float* b1 = reinterpret_cast<const float*>(layer + kOffBff1);
-  const float* b2 = reinterpret_cast<const float*>(layer + kOffBff2);
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int64_t tok = (int64_t(blockIdx.x) * kMlpWaves + wave) * 32 + j;
@@ -936,55 +1098,54 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
   float* xr = X + trow * kDim;
   uint16_t* nr = xn + trow * kDim;
 
+  // With the out-projection, X joins the accumulators one 32-row tile per stage (its loads spread over
+  // the stages instead of all waves of the chip loading it at once); without it, they start at X.
   f32x16 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(xr + 32 * t + row_of_group(g, hh));
+      const f32x4 x = OUTPROJ ? f32x4{0.f, 0.f, 0.f, 0.f}
+                              : *reinterpret_cast<const f32x4*>(xr + 32 * t + row_of_group(g, hh));
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[t][4 * g + r] = x[r];
     }
 
   constexpr int s_begin = OUTPROJ ? 0 : kOutStages;
-  constexpr int s_end = FF ? kOutStages + kFfStages : kOutStages;  // stages: W_out k-steps, then hidden tiles
-  auto issue = [&](int s, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int b = wave * 4 + i;  // 32 blocks per stage
-      const u32x4* src;
-      if (s < kOutStages) {
-        src = wo + (int64_t(b >> 2) * 32 + 4 * s + (b & 3)) * 64;  // W_out tile b/4, k-step 4s + b%4
-      } else {
-        const int ht = s - kOutStages;
-        src = b < 16 ? w1 + (int64_t(ht) * 16 + b) * 64                             // W1 tile ht, k-step b
-                     : w2 + (int64_t((b - 16) >> 1) * 64 + 2 * ht + (b & 1)) * 64;  // W2 tile (b-16)/2, k-step 2ht + b%2
-      }
-      lds_load_block(src, &lds[buf][b * 64], lane);
-    }
-  };
-
-  issue(s_begin, 0);
+  constexpr int s_end = FF ? kOutStages + kFfStages + 1 : kOutStages;
+  if (FF && wave < 4)  // b1 (4 KB) and b2 (1 KB) into LDS; the first stage barrier waits for them
+    lds_load_block(reinterpret_cast<const u32x4*>(layer + kOffBff1) + wave * 64, &bias[wave * 64], lane);
+  if (FF && wave == 4) lds_load_block(reinterpret_cast<const u32x4*>(layer + kOffBff2), &bias[kHidden / 4], lane);
+  mlp_issue(s_begin, lds[0], wo, w1, w2, wave, lane);
   if (OUTPROJ) {
     const uint16_t* orow = O + trow * 512;
-    u32x4 ob[4];
+    u32x4 ob[4];  // O operands of the next stage
     auto load_o = [&](int s) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) ob[i] = reinterpret_cast<const u32x4*>(orow)[2 * (4 * s + i) + hh];
     };
+    f32x4 xt[4];  // X tile of the next stage
+    auto load_x = [&](int t) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) xt[g] = *reinterpret_cast<const f32x4*>(xr + 32 * t + row_of_group(g, hh));
+    };
     load_o(0);
+    load_x(0);
+#pragma unroll
     for (int s = 0; s < kOutStages; ++s) {
       stage_barrier();
-      if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
-      const u32x4* Ls = lds[s & 1];
-      u32x4 cur[4] = {ob[0], ob[1], ob[2], ob[3]};
-      if (s + 1 < kOutStages) load_o(s + 1);
-#pragma unroll
-      for (int ksl = 0; ksl < 4; ++ksl) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[t] = mfma32(Ls[(t * 4 + ksl) * 64 + lane], cur[ksl], acc[t]);
-        __builtin_amdgcn_sched_barrier(0);  // bound the LDS operands in flight (register budget)
+      if (s + 1 < s_end) mlp_issue(s + 1, lds[(s + 1) & 1], wo, w1, w2, wave, lane);
+      const u32x4 cur[4] = {ob[0], ob[1], ob[2], ob[3]};
+      const f32x4 xs[4] = {xt[0], xt[1], xt[2], xt[3]};
+      if (s + 1 < kOutStages) {
+        load_o(s + 1);
+        load_x(s + 1);
       }
+      mlp_out_block(lds[s & 1], cur, lane, acc);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[s][4 * g + r] += xs[g][r];
     }
   }
   const float inv = acc_inv_norm(acc, eps);
@@ -1001,49 +1162,16 @@ __global__ __launch_bounds__(512) void k_mlp(const uint16_t* __restrict__ O, con
                    pk_ff<F16>(acc[t][4 * g0 + 4] * inv, acc[t][4 * g0 + 5] * inv),
                    pk_ff<F16>(acc[t][4 * g0 + 6] * inv, acc[t][4 * g0 + 7] * inv)};
   }
+  const f32x4* bf = reinterpret_cast<const f32x4*>(bias);
+  mlp_ff_stages<F16>(acc, xb, lds, bf, wo, w1, w2, wave, lane, hh);
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {  // + b2, a few bias vectors at a time (the accumulators fill most registers)
+  for (int t = 0; t < 8; ++t)  // + b2
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const f32x4 b = *reinterpret_cast<const f32x4*>(b2 + 32 * t + row_of_group(g, hh));
+      const f32x4 b = bf[kHidden / 4 + 8 * t + 2 * g + hh];
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[t][4 * g + r] += b[r];
     }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  for (int s = kOutStages; s < s_end; ++s) {
-    const int ht = s - kOutStages;
-    f32x4 bb[4];  // b1 of this hidden tile, loaded before the next stage is issued (see stage_barrier)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) bb[g] = *reinterpret_cast<const f32x4*>(b1 + 32 * ht + row_of_group(g, hh));
-    stage_barrier();
-    if (s + 1 < s_end) issue(s + 1, (s + 1) & 1);
-    const u32x4* Ls = lds[s & 1];
-    f32x16 h = zero16();
-#pragma unroll
-    for (int kg = 0; kg < 4; ++kg) {
-#pragma unroll
-      for (int ks = 4 * kg; ks < 4 * kg + 4; ++ks) h = mfma_ff<F16>(Ls[ks * 64 + lane], xb[ks], h);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    u32x4 hb[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float v[8];
-#pragma unroll
-      for (int gg = 0; gg < 2; ++gg)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[4 * gg + r] = gelu_erf(h[8 * c + 4 * gg + r] + bb[2 * c + gg][r]);
-      hb[c] = u32x4{pk_ff<F16>(v[0], v[1]), pk_ff<F16>(v[2], v[3]), pk_ff<F16>(v[4], v[5]), pk_ff<F16>(v[6], v[7])};
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ot = 0; ot < 8; ++ot) {
-      acc[ot] = mfma_ff<F16>(Ls[(16 + 2 * ot) * 64 + lane], hb[0], acc[ot]);
-      acc[ot] = mfma_ff<F16>(Ls[(17 + 2 * ot) * 64 + lane], hb[1], acc[ot]);
-      if (ot & 1) __builtin_amdgcn_sched_barrier(0);
-    }
-  }
   const float inv2 = acc_inv_norm(acc, eps);
   if (valid) store_row(acc, inv2, xr, nr, hh);
 }
