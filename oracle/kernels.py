@@ -87,10 +87,17 @@ def qkv_rope(xn: Tensor, W: Tensor, b_gate: Tensor, freqs: Tensor, mode: int, ba
 
 
 def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int, T: int, F: int,
-              chunk: int = 64) -> Tensor:
-    """attention (kernels.cpp:250-388): exact row max over valid keys, e = 2^(s - m) in fp32 (Q carries
+              chunk: int = 64, shift: str = "device") -> Tensor:
+    """attention (kernels.cpp:250-388): exact row max m over valid keys, e = 2^(s - m) in fp32 (Q carries
     log2(e), see qkv_rope), unnormalised bf16 P, fp32 row sum of e, O = (P V) * gate / sum rounded to
-    bf16, token order."""
+    bf16, token order.
+
+    ``shift="max"`` is the reference's shift m.  ``shift="device"`` follows the library: sequences of more
+    than 64 positions go through the single-sweep kernel, whose shift is an integer >= m; with an integer
+    shift P = 2^-c bf16(2^s), so every integer gives the same result and ceil(m) stands for it here.
+    Sequences of up to 64 positions keep m."""
+    if shift not in ("device", "max"):
+        raise ValueError("shift must be 'device' or 'max'")
     idx = token_index(mode, batch, T, F)
     nseq, L = idx.shape
     Q, K = qk_rows(Q), qk_rows(K)
@@ -102,6 +109,8 @@ def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int
         v = Vt[s0:s1, :, :, :L].double().transpose(-1, -2)
         S = (q @ k.transpose(-1, -2)).float()
         m = S.amax(dim=-1, keepdim=True)
+        if shift == "device" and L > 64:
+            m = torch.ceil(m)
         e = torch.exp2(S - m)  # fp32
         rs = e.double().sum(dim=-1, keepdim=True)
         o = e.to(torch.bfloat16).double() @ v  # [s, H, L, DH]

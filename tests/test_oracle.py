@@ -144,6 +144,57 @@ def test_emulated_attention_rows_and_gate():
     assert (O[:, :, 5:] == 0).all()
 
 
+def test_integer_softmax_shift_commutes_with_bf16_rounding():
+    """The long-sequence kernel shifts scores by an integer c instead of the row max: bf16(2^(s-c)) is
+    exactly 2^-c bf16(2^s) for any integer c in range, so the normalised result cannot depend on c."""
+    s = torch.randn(4096, generator=torch.Generator().manual_seed(11)) * 6.0
+    base = torch.exp2(s).to(torch.bfloat16).double()
+    for c in (-20, -3, 0, 1, 7, 40):
+        shifted = torch.exp2(s - float(c)).to(torch.bfloat16).double()
+        assert torch.equal(shifted * 2.0**c, base), c
+    # a fractional shift (the row max itself) moves the roundings: they differ somewhere
+    m = float(s.max())
+    frac = torch.exp2(s - m).to(torch.bfloat16).double() * 2.0**m
+    assert not torch.equal(frac, base)
+
+
+def _exact_attention(Q, K, Vt, G, mode, batch, T, F_):
+    """Textbook fp64 softmax attention on the same bf16 operands (no bf16 P), [ntok, 512]."""
+    L = T if mode == 0 else F_
+    idx = ok.token_index(mode, batch, T, F_)
+    q, k = ok.qk_rows(Q)[:, :, :L].double(), ok.qk_rows(K)[:, :, :L].double()
+    v = Vt[:, :, :, :L].double().transpose(-1, -2)
+    o = torch.softmax((q @ k.transpose(-1, -2)) * math.log(2.0), dim=-1) @ v  # Q carries log2(e)
+    o = o * G[idx].permute(0, 2, 1).unsqueeze(-1).double()
+    n = batch * T * F_
+    out = torch.empty(n, 8, 64, dtype=torch.float64)
+    out[idx] = o.permute(0, 2, 1, 3)
+    return out.view(n, 512)
+
+
+@pytest.mark.parametrize("scale", [0.2, 0.6, 1.0])
+def test_device_shift_as_accurate_as_reference_shift(scale):
+    """Long sequences: the library's integer shift against the reference's row-max shift, both measured
+    against exact fp64 attention.  With the row max the dominant key's P is exactly 1; with an integer
+    shift it is rounded like the others, so peaked rows (larger scale: scores spanning ~10-30 units) lose
+    up to ~3 dB at this op; flat rows lose nothing."""
+    g = torch.Generator().manual_seed(12)
+    batch, T, F_ = 1, 150, 2
+    xn = torch.nn.functional.normalize(torch.randn(T * F_, 256, generator=g), dim=-1).to(torch.bfloat16)
+    W = (scale * torch.randn(1544, 256, generator=g)).to(torch.bfloat16)
+    Q, K, Vt, G = ok.qkv_rope(xn, W, torch.zeros(8), weights.rotary_freqs(), 0, batch, T, F_)
+    exact = _exact_attention(Q, K, Vt, G, 0, batch, T, F_).numpy()
+    dev = ok.attention(Q, K, Vt, G, 0, batch, T, F_).double()
+    ref = ok.attention(Q, K, Vt, G, 0, batch, T, F_, shift="max").double()
+    assert not torch.equal(dev, ref)
+    s_dev, s_ref = snr_db(exact, dev.numpy()), snr_db(exact, ref.numpy())
+    assert s_dev >= 50.0 and s_dev >= s_ref - 3.5, (s_dev, s_ref)
+    assert snr_db(ref.numpy(), dev.numpy()) >= 48.0
+    # short sequences (<= 64 positions) keep the row max
+    Qs, Ks, Vts, Gs = ok.qkv_rope(xn[:60], W, torch.zeros(8), weights.rotary_freqs(), 1, 1, 1, 60)
+    assert torch.equal(ok.attention(Qs, Ks, Vts, Gs, 1, 1, 1, 60), ok.attention(Qs, Ks, Vts, Gs, 1, 1, 1, 60, shift="max"))
+
+
 def test_kernel_emulation_pads_and_layouts():
     g = torch.Generator().manual_seed(6)
     n, T, F_ = 2 * 3 * 70, 3, 70

@@ -447,15 +447,17 @@ __device__ __forceinline__ void attn_store(const f32x16 (&o)[2], int q, int L, i
     }
 }
 
-// Long sequences (time attention, L up to a few thousand).  Exact, non-online softmax in two passes
-// (kernels.cpp:286-384): pass 1 sweeps all keys for the row max m; pass 2 recomputes the scores, forms
-// e = 2^(s - m) (q carries the factor log2(e), so scores are base-2 exponents), sums e in fp32, rounds
-// P = e to bf16 unnormalised and accumulates P.V; the epilogue scales by gate/sum.
+// Long sequences (time attention, L up to a few thousand).  The reference's exact, non-online softmax
+// (kernels.cpp:286-384) first finds the row max m, then forms e = 2^(s - m) (q carries the factor
+// log2(e), so scores are base-2 exponents), sums e in fp32, rounds P = e to bf16 unnormalised and
+// accumulates P.V; the epilogue scales by gate/sum.  Here one sweep over the keys does the same with an
+// integer shift c >= the running max in place of m (see kAttHeadroom): a power-of-two shift changes
+// neither the bf16 rounding of P nor the normalised result, and QK^T is computed once instead of twice.
 // One workgroup = one (sequence, head) and 4 waves x 64 queries; each wave holds two 32-query column
-// tiles, so every K or V^T operand read from LDS feeds two MFMAs.  Tiles of 64 keys of K and V^T are
-// double-buffered in LDS, loaded global->LDS directly, with the XOR swizzle of the 16-byte chunks
-// (bank-conflict-free operand reads) applied through each lane's source address.  Only the last key
-// tile can hold keys >= L, so the masked code runs once per pass.
+// tiles, so every K or V^T operand read from LDS feeds two MFMAs.  Tiles of 64 keys of K and V^T stream
+// through a ring of LDS buffers, loaded global->LDS directly (V^T with the XOR swizzle of its 16-byte
+// chunks applied through each lane's source address, for bank-conflict-free operand reads).  Only the
+// last key tile can hold keys >= L, so the masked code runs once.
 constexpr int kAttWaves = 4;
 constexpr int kAttQT = 2;                       // 32-query column tiles per wave
 constexpr int kAttBlockQ = kAttWaves * 32 * kAttQT;  // queries per workgroup
@@ -499,32 +501,64 @@ __device__ __forceinline__ void load_k_half(const u32x4* __restrict__ Kl, int kh
   for (int ks = 0; ks < 4; ++ks) ka[ks] = Kl[(2 * ks + hh) * 64 + 32 * kh + j];
 }
 
-// Pass-1 work of one 64-key tile: scores for both query tiles, running max.
-template <bool MASK>
-__device__ __forceinline__ void attn_max_tile(const u32x4* __restrict__ Kl, const u32x4 (&qb)[kAttQT][4], int key0,
-                                              int L, int j, int hh, float (&m)[kAttQT]) {
-#pragma unroll
-  for (int kh = 0; kh < 2; ++kh) {
-    u32x4 ka[4];
-    load_k_half(Kl, kh, j, hh, ka);
-#pragma unroll
-    for (int qt = 0; qt < kAttQT; ++qt) {
-      f32x16 sacc = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[qt][ks], sacc);
-      m[qt] = MASK ? block_max(sacc, key0 + 32 * kh, L, hh, m[qt]) : block_max(sacc, 0, 32, hh, m[qt]);
-    }
-  }
+// Softmax shift of the single pass.  Scores are base-2 exponents; the shift c of a query is an integer,
+// set from the first 32 keys and raised (never lowered) whenever a score exceeds it, to kAttHeadroom
+// above the running max.  Raising c by d scales the earlier probabilities, their sum and the P.V
+// accumulators by 2^-d: exact in fp32, and it commutes with the bf16 rounding of P.  With an integer
+// shift, P = bf16(2^(s-c)) = 2^-c bf16(2^s), so the normalised result does not depend on which integer
+// c is (up to the fp32 rounding of s - c): it is the non-online softmax of the reference with the
+// row max m replaced by an integer >= m, which only moves P's bf16 rounding by the factor 2^(m - ceil m).
+// The final c is within kAttHeadroom + 1 of the row max, so the largest probability stays >=
+// 2^-(kAttHeadroom+1) and nothing of the fp32/bf16 range is lost.
+constexpr float kAttHeadroom = 8.0f;
+
+// max of x over lanes l and l ^ 32: v_permlane32_swap exchanges the half-waves, so of its two results
+// one is x and the other the partner's value, in either order.
+__device__ __forceinline__ float halfwave_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Pass-2 work of one 64-key tile: scores, exact-softmax probabilities, P.V accumulation.
-// The score accumulators start at -m (negm: the row max of this lane's query in all 16 registers),
-// so the MFMAs deliver s - m and the softmax needs no subtraction.
-template <bool MASK>
-__device__ __forceinline__ void attn_pv_tile(const u32x4* __restrict__ Kl, const u32x4* __restrict__ Vl,
-                                             const u32x4 (&qb)[kAttQT][4], int key0, int L, int j, int hh,
-                                             const f32x16 (&negm)[kAttQT], float (&lsum)[kAttQT],
-                                             f32x16 (&o)[kAttQT][2]) {
+// One 32-key half of a tile for one 32-query column tile: S^T = K.Q^T accumulated onto -c, the shift
+// raised if a score exceeds it, then P = 2^(s - c) as two B operands and the fp32 sum.  FIRST (the
+// first half of tile 0, 32 valid keys) sets c from its own row max.
+template <bool FIRST, bool MASK>
+__device__ __forceinline__ void attn_half(const u32x4 (&ka)[4], const u32x4 (&qb)[4], int key0, int L, int hh,
+                                          f32x16& negc, float& lsum, f32x16 (&o)[2], u32x4& p0, u32x4& p1) {
+  f32x16 sacc = FIRST ? zero16() : negc;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[ks], sacc);
+  float hm = MASK ? block_max(sacc, key0, L, hh, -INFINITY) : block_max(sacc, 0, 32, hh, -INFINITY);
+  hm = halfwave_max(hm);  // the query's 32 keys sit in lanes j and j + 32
+  if (FIRST) {
+    const float c = ceilf(hm) + kAttHeadroom;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      negc[r] = -c;
+      sacc[r] -= c;
+    }
+  } else if (__any(hm > 0.f)) {  // a score above the shift somewhere in the wave (rare)
+    const float d = hm > 0.f ? ceilf(hm) + kAttHeadroom : 0.f;
+    const int di = int(d);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      negc[r] -= d;
+      sacc[r] -= d;
+    }
+    lsum = ldexpf(lsum, -di);
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = ldexpf(o[dt][r], -di);
+  }
+  softmax_block(sacc, MASK ? key0 : 0, MASK ? L : 32, hh, 0.0f, lsum, p0, p1);
+}
+
+// One 64-key tile: per 32-key half, scores and probabilities for both query tiles, then P.V.
+template <bool FIRST, bool MASK>
+__device__ __forceinline__ void attn_tile(const u32x4* __restrict__ Kl, const u32x4* __restrict__ Vl,
+                                          const u32x4 (&qb)[kAttQT][4], int key0, int L, int j, int hh,
+                                          f32x16 (&negc)[kAttQT], float (&lsum)[kAttQT], f32x16 (&o)[kAttQT][2]) {
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
     u32x4 ka[4];
@@ -532,10 +566,10 @@ __device__ __forceinline__ void attn_pv_tile(const u32x4* __restrict__ Kl, const
     u32x4 p0[kAttQT], p1[kAttQT];
 #pragma unroll
     for (int qt = 0; qt < kAttQT; ++qt) {
-      f32x16 sacc = negm[qt];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[qt][ks], sacc);
-      softmax_block(sacc, MASK ? key0 + 32 * kh : 0, MASK ? L : 32, hh, 0.0f, lsum[qt], p0[qt], p1[qt]);
+      if (FIRST && kh == 0)
+        attn_half<true, false>(ka, qb[qt], 0, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
+      else
+        attn_half<false, MASK>(ka, qb[qt], key0 + 32 * kh, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
     }
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -596,48 +630,27 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
       qb[qt][ks] = q < Lpad ? *reinterpret_cast<const u32x4*>(Qh + (int64_t(2 * ks + hh) * Lpad + q) * 8) : zero4();
   }
 
-  const int nkt = Lpad / 64;
-  // ---- pass 1: exact row max over all valid keys
-  float m[kAttQT];
-#pragma unroll
-  for (int qt = 0; qt < kAttQT; ++qt) m[qt] = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kAttBufs - 1; ++i)
-    if (i < nkt) stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
-  for (int kt = 0; kt < nkt; ++kt) {
-    if (kt + kAttBufs - 2 < nkt)  // the younger tiles kt+1 .. kt+kAttBufs-2 are in flight: 2 loads each
-      tile_barrier<2 * (kAttBufs - 2)>();
-    else
-      tile_barrier<0>();
-    if (kt + kAttBufs - 1 < nkt) stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[(kt + kAttBufs - 1) % kAttBufs][0], wave, lane);
-    if (!active) continue;
-    if (kt + 1 < nkt)
-      attn_max_tile<false>(lds[kt % kAttBufs][0], qb, 0, L, j, hh, m);
-    else
-      attn_max_tile<true>(lds[kt % kAttBufs][0], qb, kt * 64, L, j, hh, m);
-  }
+  const int nkt = Lpad / 64;  // >= 2: this kernel runs for L > 64
   float lsum[kAttQT];
-  f32x16 negm[kAttQT];
+  f32x16 negc[kAttQT], o[kAttQT][2];
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt) {
-    m[qt] = fmaxf(m[qt], __shfl_xor(m[qt], 32));
     lsum[qt] = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) negm[qt][r] = -m[qt];
+    negc[qt] = o[qt][0] = o[qt][1] = zero16();
   }
-
-  // ---- pass 2: probabilities and P.V
-  f32x16 o[kAttQT][2];
-#pragma unroll
-  for (int qt = 0; qt < kAttQT; ++qt) o[qt][0] = o[qt][1] = zero16();
-  tile_barrier<0>();  // everyone is done with the pass-1 buffers before they are overwritten
 #pragma unroll
   for (int i = 0; i < kAttBufs - 1; ++i)
     if (i < nkt) {
       stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
       stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
     }
-  for (int kt = 0; kt < nkt - 1; ++kt) {
+  tile_barrier<4 * (kAttBufs - 2)>();  // tile 0 (nkt >= 2 >= kAttBufs - 1)
+  if (kAttBufs - 1 < nkt) {
+    stage_k_tile(Kh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][0], wave, lane);
+    stage_v_tile(Vh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][1], wave, lane);
+  }
+  if (active) attn_tile<true, false>(lds[0][0], lds[0][1], qb, 0, L, j, hh, negc, lsum, o);
+  for (int kt = 1; kt < nkt - 1; ++kt) {
     if (kt + kAttBufs - 2 < nkt)  // K and V: 4 loads per younger tile in flight
       tile_barrier<4 * (kAttBufs - 2)>();
     else
@@ -647,12 +660,12 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
       stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[b][0], wave, lane);
       stage_v_tile(Vh, kt + kAttBufs - 1, Lpad, lds[b][1], wave, lane);
     }
-    if (active) attn_pv_tile<false>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negm, lsum, o);
+    if (active) attn_tile<false, false>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negc, lsum, o);
   }
   tile_barrier<0>();
   if (!active) return;
-  attn_pv_tile<true>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L, j, hh,
-                     negm, lsum, o);
+  attn_tile<false, true>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L, j, hh,
+                         negc, lsum, o);
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt)
     attn_store(o[qt], q0 + 32 * qt + j, L, s, h, hh, mode, T, F, G, lsum[qt] + __shfl_xor(lsum[qt], 32), O);
