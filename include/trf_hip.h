@@ -4,11 +4,13 @@
  * The library replaces the seven AVX512-BF16 torch ops of LoggeL/turbo-roformer
  * (src/turbo_roformer/csrc/kernels.cpp:644-652) and the stack loop that calls them
  * (FastBSRoformer._transformer_cpp, src/turbo_roformer/fast.py:269-341) with HIP
- * kernels.  Every entry point takes plain device pointers, sizes and a HIP stream;
+ * kernels, and the mask head that follows the stack (FastBSRoformer._mask, fast.py:349-360).
+ * Every entry point takes plain device pointers, sizes and a HIP stream;
  * no torch type appears in a signature.  The library allocates no memory and keeps
  * no state beyond a thread-local error string: the caller owns every buffer.
  *
- * Shapes are fixed by the model: dim 256, 8 heads x 64, FF hidden 1024.
+ * Shapes are fixed by the model: dim 256, 8 heads x 64, FF hidden 1024 (the mask head's
+ * band widths and hidden size are arguments).
  *
  * Token order.  The residual stream X is fp32 [batch * T * F, 256] with token index
  *     tok = (c * T + t) * F + f        (chunk c, frame t, band f)
@@ -38,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 2
+#define TRF_ABI_VERSION 3
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -203,6 +205,51 @@ int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pa
  * model.py:142), with the FF GEMMs in the given trf_precision. */
 int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer,
                  int32_t precision, void* workspace, size_t workspace_bytes, trf_stream_t stream);
+
+/* ---------------------------------------------------------------- mask head
+ * The step after the stack: final RMSNorm and, per band f of width dins[f] (its mask columns:
+ * 2 * frequencies * channels), the mask-estimator MLP
+ *     mask_f = GLU(W2_f tanh(W1_f xn + b1_f) + b2_f),   xn = x / max(|x|, 1e-12) * sqrt(256) * gamma
+ * (MaskEstimator, model.py:158-178, mask_estimator_depth 2; the reference's batched form is
+ * FastBSRoformer._mask, fast.py:139-160 and 349-360, called at fast.py:385-387).  The mask row of a
+ * frame is the bands' outputs side by side: [n_frames][sum(dins)] fp32, band f at columns
+ * sum(dins[:f]) .. + dins[f], each the GLU a * sigmoid(g) of W2's first and second dins[f] rows.
+ *
+ * Limits: 1 <= n_bands <= 64; hidden a multiple of 64 in [64, 8192]; each din a multiple of 4 in
+ * [4, 16384]; at most 192 jobs, a job being up to 6 output pairs (64 columns: 32 of a, 32 of g) of
+ * a band, i.e. sum over bands of ceil(ceil(din / 32) / 6) <= 192. */
+
+enum trf_mask_precision {
+  /* Both GEMMs on fp16 MFMA with every operand split into hi = f16(v) and lo = f16(v - hi),
+   * hi.hi + hi.lo + lo.hi: fp32-level agreement with the reference's fp32 mask head (default). */
+  TRF_MASK_SPLIT = 0,
+  /* fp16 operands, one MFMA per product: ~3x fewer MFMAs, ~68 dB mask SNR against fp32. */
+  TRF_MASK_FP16 = 1
+};
+
+/* One band's plain fp32 weights, device pointers, PyTorch Linear layout [out][in]:
+ * mask_estimators.0.to_freqs.<f>.0.0.{weight,bias} and .0.2.{weight,bias}. */
+typedef struct trf_mask_band_src {
+  const float* w1; /* [hidden][256] */
+  const float* b1; /* [hidden] */
+  const float* w2; /* [2 * din][hidden] */
+  const float* b2; /* [2 * din] */
+} trf_mask_band_src;
+
+/* Bytes of the packed mask head (0 if the arguments are out of the limits above). */
+size_t trf_mask_head_packed_bytes(const int32_t* dins, int32_t n_bands, int32_t hidden);
+
+/* Pack the band MLPs (bands: host array of n_bands; dins: host array) and the final norm's gamma
+ * (device fp32 [256], final_norm.gamma) into packed (device, trf_mask_head_packed_bytes(),
+ * 16-byte aligned).  |w1 * gamma| and |w2| must be below 65504 (fp16 range). */
+int trf_pack_mask_head(const trf_mask_band_src* bands, const int32_t* dins, int32_t n_bands,
+                       int32_t hidden, const float* final_gamma, void* packed, trf_stream_t stream);
+
+/* mask [n_frames][sum(dins)] fp32 from the stack output X [n_frames][n_bands][256] fp32 (token
+ * order of the stack: frame-major, band-minor), precision a trf_mask_precision value.  dins,
+ * n_bands and hidden must be those of the packing.  n_frames = 0 does nothing. */
+int trf_mask_head(const float* X, int32_t n_frames, int32_t n_bands, const int32_t* dins, int32_t hidden,
+                  const void* packed, int32_t precision, float* mask, trf_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -200,3 +200,41 @@ def stack(X: Tensor, layers: list[dict], batch: int, T: int, F: int, precision: 
         Hh = gemm_gelu(xn, w["W1"], w["b1"])
         X, xn = gemm_res_norm(Hh, w["W2"], w["b2"], X)
     return X
+
+
+def _split_f16(v: Tensor) -> tuple[Tensor, Tensor]:
+    """v (fp32) -> fp16 hi = f16(v) and lo = f16(v - hi), both returned as float64."""
+    v = v.float()
+    hi = v.half()
+    return hi.double(), (v - hi.float()).half().double()
+
+
+def _mm_f16(a: Tensor, w: Tensor, split: bool) -> Tensor:
+    """a @ w^T with fp16 operands and fp64 sums: hi.hi + hi.lo + lo.hi when split, else hi.hi."""
+    ah, al = _split_f16(a)
+    wh, wl = _split_f16(w)
+    out = ah @ wh.t()
+    if split:
+        out = out + al @ wh.t() + ah @ wl.t()
+    return out
+
+
+@torch.no_grad()
+def mask_head(x: Tensor, sd, dims: tuple[int, ...], precision: str = "split") -> Tensor:
+    """Final RMSNorm + per-band mask MLP (fast.py:349-360, model.py:158-178) at the rounding points of the
+    library's trf_mask_head: xn = x / max(|x|, 1e-12) * 16 in fp32, W1 * gamma folded in fp32, then xn,
+    W1, tanh(h) and W2 rounded to fp16 hi (and lo = f16(v - hi) with ``precision="split"``), products
+    hi.hi (+ hi.lo + lo.hi) summed in fp64, biases and GLU in fp64.  Not a reference kernel: the library's
+    own arithmetic.  x: (..., bands, 256) -> (..., sum(dims))."""
+    split = precision == "split"
+    xf = x.float()
+    xn = (xf / xf.norm(dim=-1, keepdim=True).clamp_min(1e-12)) * DIM**0.5
+    g = sd["final_norm.gamma"].float()
+    outs = []
+    for i, d in enumerate(dims):
+        p = f"mask_estimators.0.to_freqs.{i}.0"
+        w1 = sd[f"{p}.0.weight"].float() * g[None, :]
+        h = torch.tanh(_mm_f16(xn[..., i, :], w1, split) + sd[f"{p}.0.bias"].double())
+        o = _mm_f16(h.float(), sd[f"{p}.2.weight"].float(), split) + sd[f"{p}.2.bias"].double()
+        outs.append(o[..., :d] * torch.sigmoid(o[..., d:]))
+    return torch.cat(outs, dim=-1)

@@ -58,3 +58,44 @@ def test_argument_errors_need_no_device(lib):
     assert b"precision" in lib.trf_last_error()
     assert lib.trf_seq_buffer_elems(2, 1, 8, 2) == -1
     assert lib.trf_stack_workspace_bytes(0, 8, 2) == 0
+
+
+def _dins(*d):
+    return (ctypes.c_int32 * len(d))(*d)
+
+
+def test_mask_head_packed_bytes(lib):
+    from turbo_roformer_amd import weights
+
+    def expect(dims, hidden):
+        w = sum((hidden // 32) * (32 + 8 * ((d + 31) // 32)) * 1024 for d in dims)
+        b1 = -(-(w + len(dims) * hidden * 4) // 256) * 256
+        return b1 + sum(-(-(2 * 32 * ((d + 31) // 32) * 4) // 256) * 256 for d in dims)
+
+    for cfg in (weights.RESURRECTION_CFG, weights.TINY_CFG):
+        dims = weights.band_dims(cfg)
+        hidden = cfg["dim"] * cfg["mlp_expansion_factor"]
+        n = lib.trf_mask_head_packed_bytes(_dins(*dims), len(dims), hidden)
+        assert n == expect(dims, hidden)
+    # full-size model: W1 hi+lo (62 x 1 MB) and W2 hi+lo for 157 output pairs of 64 columns
+    assert lib.trf_mask_head_packed_bytes(_dins(*weights.band_dims(weights.RESURRECTION_CFG)), 62, 1024) > 100 << 20
+
+
+def test_mask_head_argument_errors_need_no_device(lib):
+    p = ctypes.c_void_p(256)
+    d = _dins(8, 16, 516)
+    assert lib.trf_mask_head_packed_bytes(d, 3, 1000) == 0  # hidden not a multiple of 64
+    assert b"hidden" in lib.trf_last_error()
+    assert lib.trf_mask_head_packed_bytes(_dins(8, 18), 2, 1024) == 0  # width not a multiple of 4
+    assert b"dins[1]" in lib.trf_last_error()
+    assert lib.trf_mask_head_packed_bytes(d, 0, 1024) == 0
+    assert lib.trf_mask_head_packed_bytes(_dins(*([16384] * 64)), 64, 1024) == 0  # 64 x 86 jobs > 192
+    assert b"jobs" in lib.trf_last_error()
+    assert lib.trf_mask_head(p, 10, 3, d, 1024, p, 2, p, None) == 1
+    assert b"precision" in lib.trf_last_error()
+    assert lib.trf_mask_head(p, -1, 3, d, 1024, p, 0, p, None) == 1
+    assert lib.trf_mask_head(p, 10, 3, d, 1024, None, 0, p, None) == 1
+    assert b"packed must not be NULL" in lib.trf_last_error()
+    assert lib.trf_mask_head(None, 0, 3, d, 1024, None, 0, None, None) == 0  # nothing to do
+    assert lib.trf_pack_mask_head(None, d, 3, 1024, p, p, None) == 1
+    assert b"bands" in lib.trf_last_error()

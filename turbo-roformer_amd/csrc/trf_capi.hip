@@ -1,10 +1,13 @@
-// C ABI of the stack (declared in include/trf_hip.h): argument checks, workspace layout and
-// the 24-sub-layer driver.  Host code only; the kernels live in trf_kernels.hip.
+// C ABI of the stack and the mask head (declared in include/trf_hip.h): argument checks, workspace and
+// packed layouts, the 24-sub-layer driver and the mask-head launch plan.  Host code only; the kernels
+// live in trf_kernels.hip and trf_mask.hip.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
+#include <vector>
 
 #include "trf_hip.h"
 #include "trf_internal.h"
@@ -165,6 +168,103 @@ int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const*
                       st, ev));
   }
   return TRF_OK;
+}
+
+// ---------------------------------------------------------------- mask head
+// Byte layout of the packed mask head (see trf_internal.h) for a list of band widths.
+struct MaskLayout {
+  int n_bands = 0, hidden = 0;
+  std::vector<int> din;
+  std::vector<size_t> wofs, b2_off;  // bytes
+  size_t b1_off = 0, total = 0;
+};
+
+int mask_npairs(int din) { return (din + 31) / 32; }
+int mask_njobs(int din) { return (mask_npairs(din) + trf::kMaskPairs - 1) / trf::kMaskPairs; }
+
+int mask_layout(const int32_t* dins, int32_t n_bands, int32_t hidden, MaskLayout& L) {
+  if (!dins) return fail(TRF_ERR_ARG, "dins must not be NULL");
+  if (n_bands < 1 || n_bands > trf::kMaskMaxBands)
+    return fail(TRF_ERR_ARG, "n_bands must be in [1, %d], got %d", trf::kMaskMaxBands, n_bands);
+  if (hidden < 64 || hidden > 8192 || hidden % 64)
+    return fail(TRF_ERR_ARG, "hidden must be a multiple of 64 in [64, 8192], got %d", hidden);
+  L = MaskLayout{};
+  L.n_bands = n_bands;
+  L.hidden = hidden;
+  int jobs = 0;
+  size_t off = 0;
+  for (int f = 0; f < n_bands; ++f) {
+    const int d = dins[f];
+    if (d < 4 || d > 16384 || d % 4)
+      return fail(TRF_ERR_ARG, "dins[%d] = %d: band widths must be multiples of 4 in [4, 16384]", f, d);
+    jobs += mask_njobs(d);
+    L.din.push_back(d);
+    L.wofs.push_back(off);
+    off += size_t(hidden / 32) * (trf::kMaskW1Blocks + 8 * mask_npairs(d)) * trf::kTileBytes;
+  }
+  if (jobs > trf::kMaskMaxJobs)
+    return fail(TRF_ERR_ARG, "the bands make %d jobs of up to %d output pairs, more than %d", jobs,
+                trf::kMaskPairs, trf::kMaskMaxJobs);
+  L.b1_off = off;
+  off = round_up(off + size_t(n_bands) * hidden * 4);
+  for (int f = 0; f < n_bands; ++f) {
+    L.b2_off.push_back(off);
+    off = round_up(off + size_t(2 * 32 * mask_npairs(L.din[f])) * 4);
+  }
+  L.total = off;
+  if (L.total >= (size_t(1) << 32)) return fail(TRF_ERR_ARG, "packed mask head would exceed 4 GiB");
+  return TRF_OK;
+}
+
+// Launch plan: each band is cut into jobs of at most kMaskPairs output pairs (as even as possible), and
+// the jobs are dealt to the XCDs largest first, each to the XCD with the least work so far (work of a job
+// ~ its MFMAs per frame: 16 k-steps of GEMM1 + 4 per output pair of GEMM2).  A workgroup of XCD x then
+// runs one job over kMaskFrames frames; the workgroups of one job on one XCD share its weights in L2.
+unsigned mask_plan(const MaskLayout& L, int32_t n_frames, trf::MaskPlan& p) {
+  p = trf::MaskPlan{};
+  p.hidden = L.hidden;
+  p.n_frames = n_frames;
+  p.F = L.n_bands;
+  p.ntb = (n_frames + trf::kMaskFrames - 1) / trf::kMaskFrames;
+  p.b1_off = uint32_t(L.b1_off);
+  struct Job {
+    uint32_t code;
+    int cost;
+  };
+  std::vector<Job> jobs;
+  int col = 0;
+  for (int f = 0; f < L.n_bands; ++f) {
+    p.wofs_kb[f] = uint32_t(L.wofs[f] / 1024);
+    p.b2_off[f] = uint32_t(L.b2_off[f]);
+    p.col[f] = uint32_t(col);
+    p.din[f] = uint16_t(L.din[f]);
+    col += L.din[f];
+    const int np = mask_npairs(L.din[f]), nj = mask_njobs(L.din[f]);
+    for (int q = 0, p0 = 0; q < nj; ++q) {
+      const int n = np / nj + (q < np % nj ? 1 : 0);
+      jobs.push_back(Job{uint32_t(f) | uint32_t(n) << 8 | uint32_t(p0) << 16, 16 + 4 * n});
+      p0 += n;
+    }
+  }
+  p.width = col;
+  std::stable_sort(jobs.begin(), jobs.end(), [](const Job& a, const Job& b) { return a.cost > b.cost; });
+  std::vector<std::vector<uint32_t>> per(trf::kXcds);
+  long load[trf::kXcds] = {};
+  for (const Job& j : jobs) {
+    int x = 0;
+    for (int y = 1; y < trf::kXcds; ++y)
+      if (load[y] < load[x]) x = y;
+    per[x].push_back(j.code);
+    load[x] += j.cost;
+  }
+  size_t most = 0, k = 0;
+  for (int x = 0; x < trf::kXcds; ++x) {
+    p.xcd_start[x] = uint32_t(k);
+    for (uint32_t c : per[x]) p.job[k++] = c;
+    most = per[x].size() > most ? per[x].size() : most;
+  }
+  p.xcd_start[trf::kXcds] = uint32_t(k);
+  return unsigned(size_t(trf::kXcds) * most * p.ntb);
 }
 
 }  // namespace
@@ -336,6 +436,52 @@ int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pack
   if (int rc = check_launch("add_rmsnorm")) return rc;
   trf::launch_ff(static_cast<const uint8_t*>(packed_layer), X, w.xn, n, precision, 1e-12f, st);
   return check_launch("feed_forward");
+}
+
+size_t trf_mask_head_packed_bytes(const int32_t* dins, int32_t n_bands, int32_t hidden) {
+  MaskLayout L;
+  if (mask_layout(dins, n_bands, hidden, L)) return 0;
+  return L.total;
+}
+
+int trf_pack_mask_head(const trf_mask_band_src* bands, const int32_t* dins, int32_t n_bands, int32_t hidden,
+                       const float* final_gamma, void* packed, trf_stream_t stream) {
+  MaskLayout L;
+  if (int rc = mask_layout(dins, n_bands, hidden, L)) return rc;
+  if (!bands) return fail(TRF_ERR_ARG, "bands must not be NULL");
+  if (!final_gamma) return fail(TRF_ERR_ARG, "final_gamma must not be NULL");
+  TRF_REQUIRE(packed, "packed");
+  for (int f = 0; f < n_bands; ++f)
+    if (!bands[f].w1 || !bands[f].b1 || !bands[f].w2 || !bands[f].b2)
+      return fail(TRF_ERR_ARG, "bands[%d] has a NULL weight pointer", f);
+  hipStream_t st = as_hip(stream);
+  uint8_t* d = static_cast<uint8_t*>(packed);
+  for (int f = 0; f < n_bands; ++f) {
+    trf::launch_pack_mask_band(bands[f].w1, final_gamma, bands[f].b1, bands[f].w2, bands[f].b2, L.din[f], hidden,
+                               d + L.wofs[f], reinterpret_cast<float*>(d + L.b1_off) + size_t(f) * hidden,
+                               reinterpret_cast<float*>(d + L.b2_off[f]), st);
+    if (int rc = check_launch("pack_mask_head")) return rc;
+  }
+  return TRF_OK;
+}
+
+int trf_mask_head(const float* X, int32_t n_frames, int32_t n_bands, const int32_t* dins, int32_t hidden,
+                  const void* packed, int32_t precision, float* mask, trf_stream_t stream) {
+  MaskLayout L;
+  if (int rc = mask_layout(dins, n_bands, hidden, L)) return rc;
+  if (precision != TRF_MASK_SPLIT && precision != TRF_MASK_FP16)
+    return fail(TRF_ERR_ARG, "precision must be 0 (split) or 1 (fp16), got %d", precision);
+  if (n_frames < 0) return fail(TRF_ERR_ARG, "n_frames must be >= 0, got %d", n_frames);
+  if (int64_t(n_frames) * n_bands >= (int64_t(1) << 31))
+    return fail(TRF_ERR_ARG, "n_frames * n_bands = %lld tokens is too large", (long long)n_frames * n_bands);
+  if (n_frames == 0) return TRF_OK;
+  TRF_REQUIRE(X, "X");
+  TRF_REQUIRE(packed, "packed");
+  TRF_REQUIRE(mask, "mask");
+  trf::MaskPlan plan;
+  const unsigned grid = mask_plan(L, n_frames, plan);
+  trf::launch_mask_head(X, static_cast<const uint8_t*>(packed), mask, plan, grid, precision, as_hip(stream));
+  return check_launch("mask_head");
 }
 
 }  // extern "C"

@@ -93,4 +93,42 @@ void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_
 // xn is written as X / |X|.
 void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, int ff_precision, float eps, hipStream_t st);
 
+// ---------------------------------------------------------------- mask head (trf_mask.hip)
+// Final norm + one MLP per band (Linear dim -> hidden, tanh, Linear hidden -> 2 din, GLU).
+// Packed weights of band b, hidden tile j (32 hidden units), in 1 KB operand blocks (fp16, 64 lanes x 8):
+//   W1 k-step s (16 inputs), hi/lo part hl:            block 2s + hl               (32 blocks)
+//   W2 output pair i, a/g half ag, k-step t, part hl:  block 32 + 8i + 4ag + 2t + hl
+// Output pair i is mask columns 32i..32i+31 of the band: its "a" tile holds W2 rows 32i+r (r < 32) and its
+// "g" tile rows din + 32i + r (zero where 32i + r >= din), so a lane holds both GLU operands of a column.
+// Tile j is (32 + 8 * npairs) KB; the tiles of a band follow each other.  Then b1 [n_bands][hidden] and,
+// per band, b2 as [a part: pad][g part: pad] (pad = 32 * npairs, zeros past din), all fp32.
+constexpr int kMaskMaxBands = 64;
+constexpr int kMaskMaxJobs = 192;
+constexpr int kMaskPairs = 6;      // output pairs per job: the largest that fits the LDS stages
+constexpr int kMaskFrames = 128;   // frames per workgroup (4 waves x 32)
+constexpr int kMaskW1Blocks = 32;  // blocks of W1 per hidden tile
+constexpr int kXcds = 8;           // workgroups are dealt round-robin over the 8 XCDs
+
+enum MaskPrecision { kMaskSplit = 0, kMaskFp16 = 1 };
+
+// Everything a mask-head launch needs besides the pointers, passed by value.  A job is (band, first
+// output pair p0, np pairs); the workgroups of XCD x run jobs job[xcd_start[x] .. xcd_start[x+1]) one
+// after the other, each over ntb blocks of kMaskFrames frames.
+struct MaskPlan {
+  int32_t hidden, n_frames, F, width, ntb;
+  uint32_t b1_off;                  // byte offset of b1 in the packed buffer
+  uint32_t xcd_start[kXcds + 1];
+  uint32_t job[kMaskMaxJobs];       // band | np << 8 | p0 << 16
+  uint32_t wofs_kb[kMaskMaxBands];  // first weight block of the band, in KB from the packed start
+  uint32_t b2_off[kMaskMaxBands];   // byte offset of the band's b2
+  uint32_t col[kMaskMaxBands];      // first mask column of the band
+  uint16_t din[kMaskMaxBands];
+};
+
+// Pack one band: W1 [hidden][kDim] (times gamma [kDim] per input), W2 [2 din][hidden], fp32 device.
+void launch_pack_mask_band(const float* w1, const float* gamma, const float* b1, const float* w2, const float* b2,
+                           int din, int hidden, uint8_t* wdst, float* b1dst, float* b2dst, hipStream_t st);
+void launch_mask_head(const float* X, const uint8_t* packed, float* mask, const MaskPlan& plan, unsigned grid,
+                      int precision, hipStream_t st);
+
 }  // namespace trf

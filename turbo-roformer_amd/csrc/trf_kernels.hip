@@ -11,60 +11,9 @@
 // Numerics follow the reference kernels (src/turbo_roformer/csrc/kernels.cpp): fp32
 // accumulators, fp32 residual stream, fp32 rotary/softmax/gate math, bf16 round-to-nearest-even
 // for every GEMM/attention operand (kernels.cpp:30-33).
-#include "trf_internal.h"
+#include "trf_device.h"
 
 namespace trf {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr float kLog2e = 1.44269504088896341f;
-
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
-  bf16x2 v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f32x16 mfma32h(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                0, 0);
-}
-
-// Two fp32 -> packed fp16 pair, round to nearest even.
-__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
-  f16x2 v = {(_Float16)lo, (_Float16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-__device__ __forceinline__ uint16_t to_bf16(float x) {
-  return __builtin_bit_cast(uint16_t, (__bf16)x);
-}
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
-
-// A zero splat: as the first accumulator of an MFMA chain it folds into the inline constant 0.
-__device__ __forceinline__ f32x16 zero16() {
-  f32x16 z = {};
-  return z;
-}
-
-__device__ __forceinline__ u32x4 zero4() {
-  u32x4 z = {0u, 0u, 0u, 0u};
-  return z;
-}
 
 // Token index of position p in sequence s (see the token-order contract in trf_hip.h).
 __device__ __forceinline__ int64_t token_of(int mode, int s, int p, int T, int F) {
@@ -74,13 +23,6 @@ __device__ __forceinline__ int64_t token_of(int mode, int s, int p, int T, int F
   }
   return int64_t(s) * F + p;
 }
-
-// Feature offset of accumulator register group g (registers 4g..4g+3) of a 32-row tile.
-__device__ __forceinline__ int row_of_group(int g, int hh) { return 8 * g + 4 * hh; }
-
-// Index of this wave in the workgroup, as a scalar (uniform) value so that addresses derived from it
-// stay in scalar registers.
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ============================================================ weight packing
 // 32x32 layouts: dst[t][ks][lane][e] = W[32t + lane%32][16ks + kperm(lane/32, e)] (kperm: natural 8hh + e,
@@ -214,24 +156,6 @@ void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_
                         hipStream_t st) {
   hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, X, Y, y_bf16, out, out_bf16,
                      n, eps);
-}
-
-// ============================================================ LDS weight streaming
-// Weights are packed as 1 KB operand blocks (one MFMA A operand: 64 lanes x 16 B).  A workgroup
-// streams the blocks of one stage into LDS with direct global->LDS loads, double-buffered: while the
-// waves compute on stage s from one buffer, the blocks of stage s+1 land in the other.
-__device__ __forceinline__ void lds_load_block(const u32x4* __restrict__ src_block, u32x4* lds_block, int lane) {
-  __builtin_amdgcn_global_load_lds(src_block + lane, lds_block, 16, 0, 0);
-}
-
-// All of this thread's outstanding global loads (direct-to-LDS ones included) have landed, and every
-// wave of the workgroup has reached this point.
-__device__ __forceinline__ void stage_barrier() {
-  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15), as the builtin so that the compiler's own waitcnt
-  // insertion knows every earlier global load has landed (an inline-asm wait is opaque to it, and it
-  // would then wait again, for the next stage's loads too, at the first use of such a value).
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
 }
 
 // ============================================================ fused QKV + gate GEMM, rotary epilogue

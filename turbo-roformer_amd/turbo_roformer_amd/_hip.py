@@ -21,12 +21,14 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
 MODE_TIME, MODE_FREQ = 0, 1
 PREC_BF16, PREC_FF_SPLIT, PREC_FF_FP16 = 0, 1, 2
 PRECISIONS = {"bf16": PREC_BF16, "ff_split": PREC_FF_SPLIT, "ff_fp16": PREC_FF_FP16}
+MASK_SPLIT, MASK_FP16 = 0, 1
+MASK_PRECISIONS = {"split": MASK_SPLIT, "fp16": MASK_FP16}
 _F32, _BF16 = 0, 1
 
 _lock = threading.Lock()
@@ -51,6 +53,12 @@ class TrfLayerSrc(ctypes.Structure):
         ("w_ff1_lo", ctypes.c_void_p),
         ("w_ff2_lo", ctypes.c_void_p),
     ]
+
+
+class TrfMaskBandSrc(ctypes.Structure):
+    """``trf_mask_band_src`` of trf_hip.h: device pointers to one band's mask-estimator MLP weights."""
+
+    _fields_ = [("w1", ctypes.c_void_p), ("b1", ctypes.c_void_p), ("w2", ctypes.c_void_p), ("b2", ctypes.c_void_p)]
 
 
 _P, _I32, _I64, _F, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
@@ -79,6 +87,11 @@ _SIGNATURES: dict[str, tuple] = {
     ),
     "trf_attn_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _P, _SZ, _P]),
     "trf_ff_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _SZ, _P]),
+    "trf_mask_head_packed_bytes": (_SZ, [ctypes.POINTER(ctypes.c_int32), _I32, _I32]),
+    "trf_pack_mask_head": (
+        ctypes.c_int, [ctypes.POINTER(TrfMaskBandSrc), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P]
+    ),
+    "trf_mask_head": (ctypes.c_int, [_P, _I32, _I32, ctypes.POINTER(ctypes.c_int32), _I32, _P, _I32, _P, _P]),
 }
 
 
@@ -376,3 +389,53 @@ def ff_block(X, batch, T, F, layer, ws, precision: str = "ff_fp16") -> None:
     _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
     _need(ws, "workspace", torch.uint8)
     _check(lib.trf_ff_block(X.data_ptr(), batch, T, F, layer.data_ptr(), prec, ws.data_ptr(), ws.numel(), _stream()))
+
+
+# ---------------------------------------------------------------------------------------------- mask head
+
+
+def _dins(dins) -> ctypes.Array:
+    return (ctypes.c_int32 * len(dins))(*[int(d) for d in dins])
+
+
+def mask_head_packed_bytes(dins, hidden: int) -> int:
+    """Bytes of the packed mask head for band widths ``dins`` and MLP hidden size ``hidden``."""
+    lib = load()
+    n = lib.trf_mask_head_packed_bytes(_dins(dins), len(dins), hidden)
+    if n == 0:
+        _check(1)
+    return int(n)
+
+
+def pack_mask_head(bands: list[tuple[torch.Tensor, ...]], dins, hidden: int, final_gamma: torch.Tensor,
+                   out: torch.Tensor) -> None:
+    """Pack per-band ``(w1 [hidden, 256], b1 [hidden], w2 [2 din, hidden], b2 [2 din])`` fp32 device
+    tensors and the final norm's gamma into ``out`` (uint8, mask_head_packed_bytes())."""
+    lib = load()
+    if len(bands) != len(dins):
+        raise ValueError("bands and dins differ in length")
+    for i, ((w1, b1, w2, b2), d) in enumerate(zip(bands, dins)):
+        _need(w1, f"w1[{i}]", torch.float32, (hidden, DIM))
+        _need(b1, f"b1[{i}]", torch.float32, (hidden,))
+        _need(w2, f"w2[{i}]", torch.float32, (2 * d, hidden))
+        _need(b2, f"b2[{i}]", torch.float32, (2 * d,))
+    _need(final_gamma, "final_gamma", torch.float32, (DIM,))
+    _need(out, "out", torch.uint8, (lib.trf_mask_head_packed_bytes(_dins(dins), len(dins), hidden),))
+    src = (TrfMaskBandSrc * len(bands))(*[TrfMaskBandSrc(*(t.data_ptr() for t in b)) for b in bands])
+    _check(lib.trf_pack_mask_head(src, _dins(dins), len(dins), hidden, final_gamma.data_ptr(), out.data_ptr(),
+                                  _stream()))
+
+
+def mask_head(X: torch.Tensor, n_frames: int, dins, hidden: int, packed: torch.Tensor, mask: torch.Tensor,
+              precision: str = "split") -> None:
+    """mask [n_frames, sum(dins)] from the stack output X [n_frames * len(dins), 256] fp32: final norm,
+    per-band Linear / tanh / Linear / GLU (fast.py:349-360)."""
+    lib = load()
+    if precision not in MASK_PRECISIONS:
+        raise ValueError(f"precision must be one of {tuple(MASK_PRECISIONS)}, got {precision!r}")
+    F = len(dins)
+    _need(X, "X", torch.float32, (n_frames * F, DIM))
+    _need(packed, "packed", torch.uint8, (lib.trf_mask_head_packed_bytes(_dins(dins), F, hidden),))
+    _need(mask, "mask", torch.float32, (n_frames, int(sum(dins))))
+    _check(lib.trf_mask_head(X.data_ptr(), n_frames, F, _dins(dins), hidden, packed.data_ptr(),
+                             MASK_PRECISIONS[precision], mask.data_ptr(), _stream()))

@@ -1,8 +1,9 @@
-"""Host path around the stack: STFT, band split, final norm + band MLP mask head, iSTFT.
+"""Host path around the stack: STFT, band split, iSTFT (and a torch mask head).
 
 These stay in PyTorch (CPU by default, any torch device works), as in ``FastBSRoformer.forward``
-(src/turbo_roformer/fast.py:363-394): only the transformer stack runs on the gfx950 kernels.  Everything
-is computed from a state dict with the reference's keys, in fp32.
+(src/turbo_roformer/fast.py:363-394).  Everything is computed from a state dict with the reference's keys,
+in fp32.  ``HostPath.mask`` is the reference's grouped-``baddbmm`` mask head in torch; the ``Separator``
+runs the mask head on the gfx950 kernels instead (``HipMaskHead``).
 """
 
 from __future__ import annotations

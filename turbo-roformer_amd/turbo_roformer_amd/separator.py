@@ -3,10 +3,11 @@
 Mirrors ``turbo_roformer.Separator.separate`` (src/turbo_roformer/separator.py:182-232): the mix is made
 stereo, short inputs are padded to whole hops, loud mixes are scaled to a 0.9 peak and back, and the song
 is cut into chunks of hop * (dim_t - 1) samples at ``overlap`` predictions per sample and recombined
-with a Hamming-windowed overlap-add.  The difference is where a chunk's forward runs: STFT, band split,
-mask head and iSTFT stay in PyTorch (``HostPath``, on the same device), and the 24-sub-layer stack of a
-whole batch of chunks is one ``trf_stack_forward`` call on the gfx950 kernels.  There is no CPU fallback:
-if the HIP library or the GPU is missing, construction raises ``HipUnavailable``.
+with a Hamming-windowed overlap-add.  The difference is where a chunk's forward runs: STFT, band split
+and iSTFT stay in PyTorch (``HostPath``, on the same device); the 24-sub-layer stack of a whole batch of
+chunks is one ``trf_stack_forward`` call and the mask head after it one ``trf_mask_head`` call on the
+gfx950 kernels.  There is no CPU fallback: if the HIP library or the GPU is missing, construction raises
+``HipUnavailable``.
 
 Out of scope here: audio files, resampling (the reference uses soxr, absent from this image) and
 surround downmix; ``separate`` takes mono or stereo float arrays at 44.1 kHz.
@@ -23,6 +24,7 @@ import torch
 from . import _hip
 from .chunking import chunk_starts, overlap_add, step_for
 from .host import HostPath
+from .mask import HipMaskHead
 from .stack import HipStack
 
 SR = 44100
@@ -54,14 +56,15 @@ class Separator:
 
     ``state_dict``/``cfg``: the model's weights (reference key names) and hyper-parameters; ``dim_t``:
     frames per chunk (chunk = hop * (dim_t - 1)); ``precision``: ``"ff_fp16"``, ``"ff_split"`` or ``"bf16"`` (see
-    ``HipStack``); ``batch_chunks``: chunks per batched stack forward (0 = the whole song at once).
+    ``HipStack``); ``mask_precision``: ``"split"`` or ``"fp16"`` (see ``HipMaskHead``); ``batch_chunks``:
+    chunks per batched stack forward (0 = the whole song at once).
     ``backend``: ``"hip"``, or ``"auto"`` which is the same here (both raise ``HipUnavailable`` when the
     kernels cannot run, like the reference's explicit ``backend="kernels"``, separator.py:147-149).
     """
 
     def __init__(self, state_dict: Mapping[str, torch.Tensor], cfg: Mapping[str, Any], dim_t: int,
                  device: str | torch.device = "cuda", precision: str = "ff_fp16", backend: str = "auto",
-                 batch_chunks: int = 0):
+                 batch_chunks: int = 0, mask_precision: str = "split"):
         if backend not in BACKENDS:
             raise ValueError(f"backend must be one of {BACKENDS}")
         ok, why = _hip.support()
@@ -74,6 +77,7 @@ class Separator:
         self.batch_chunks = int(batch_chunks)
         self.host = HostPath(state_dict, cfg, self.device)
         self.stack = HipStack(state_dict, self.device, precision)
+        self.mask_head = HipMaskHead(state_dict, cfg, self.device, mask_precision)
 
     def n_chunks(self, n_samples: int, overlap: float = 2.0) -> int:
         """Number of chunks the song is cut into (separator.py:182-186)."""
@@ -88,7 +92,7 @@ class Separator:
         b, T, F, d = X.shape
         Xd = X.reshape(b * T * F, d).contiguous()
         self.stack(Xd, b, T, F)
-        mask = self.host.mask(Xd.view(b, T, F, d))
+        mask = self.mask_head(Xd, b * T).view(b, T, -1)
         return self.host.apply(raw, mask)
 
     @torch.inference_mode()
