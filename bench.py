@@ -10,9 +10,12 @@ peak (measured with HIP events on the launch stream over the timed region), and 
 fp32 restructured torch path (the oracle) timed on the host's cores for one stack forward of the same
 chunk, whose output also gives the mask SNR of the GPU path.
 
-It also separates a synthetic 4:12 song end to end (29 chunks in one batched stack forward, host STFT /
-band split / mask head / iSTFT in PyTorch on the GPU, overlap-add on the CPU) and reports its real-time
-factor.
+The mask head after the stack (final norm + 62 band MLPs + GLU, one HIP kernel) is timed on the chunk's
+stack output beside it, with its own CPU time (the oracle's fp32 mask estimator) and accuracy.
+
+It also separates a synthetic 4:12 song end to end (29 chunks in one batched stack forward and one
+mask-head launch on the GPU, host STFT / band split / iSTFT in PyTorch on the GPU, overlap-add on the CPU)
+and reports its real-time factor.
 
     python bench.py [--steps K] [--warmup W] [--precision ff_fp16|ff_split|bf16] [--no-cpu] [--no-song]
 """
@@ -162,6 +165,30 @@ def main() -> int:
 
     ms, kernel_ms, out_gpu = timed(a.precision, True)
     alts = {p: timed(p, False) for p in ("ff_fp16", "ff_split", "bf16") if p != a.precision}
+
+    # the mask head after the stack, on this chunk's stack output (HIP events on its launch stream)
+    from turbo_roformer_amd.mask import HipMaskHead
+
+    head = HipMaskHead(sd, cfg, "cuda")
+    mask_of = lambda x: head(x.reshape(-1, 256).contiguous().cuda(), x.shape[1]).cpu().view(1, x.shape[1], -1)
+    xg = out_gpu.reshape(-1, 256).cuda()
+    mask_buf = torch.empty(T, head.width, device="cuda")
+    for _ in range(3):
+        head(xg, T, mask_buf)
+    torch.cuda.synchronize()
+    m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    m0.record()
+    for _ in range(reps):
+        head(xg, T, mask_buf)
+    m1.record()
+    torch.cuda.synchronize()
+    mask_ms = m0.elapsed_time(m1) / reps
+    mask_flops = 2 * T * (F * 256 * head.hidden + head.hidden * 2 * head.width)
+    result_mask = {"kernel": "mask head (final norm + 62 band MLPs + GLU), split-fp16 MFMA", "ms_per_chunk": round(mask_ms, 4),
+                   "gflop_per_chunk": round(mask_flops / 1e9, 2),
+                   "tflops": round(mask_flops / (mask_ms * 1e-3) / 1e12, 1)}
+    del xg, mask_buf
     attn_t_ms = kernel_ms["attention_t"]
     flops_t = attn_flops(F, T)
     achieved = flops_t / (attn_t_ms * 1e-3) / 1e12
@@ -198,11 +225,12 @@ def main() -> int:
         "kernels_ms_per_launch": {k: round(v, 4) for k, v in sorted(kernel_ms.items())},
         "precision": a.precision,
         "other_precisions": {p: {"ms_per_step": round(v[0], 4), "value": round(1e3 / v[0], 3)} for p, v in alts.items()},
+        "mask_head": result_mask,
     }
 
     if not a.no_song:
         # whole synthetic 4:12 song: 29 chunks of 17 s at overlap 2, one batched stack forward, host STFT,
-        # band split, mask head and iSTFT in PyTorch on the same GPU, Hamming overlap-add on the CPU
+        # band split and iSTFT in PyTorch and one mask-head launch on the same GPU, Hamming overlap-add on the CPU
         from turbo_roformer_amd.separator import Separator
 
         sep = Separator(sd, cfg, T, "cuda", precision=a.precision)
@@ -230,11 +258,17 @@ def main() -> int:
         t3 = time.perf_counter()
         cpu_s = t3 - t2
         snr_x = signals.snr_db(ref.numpy(), out_gpu.numpy())
+        t5 = time.perf_counter()
         m_ref = reference.mask_from_stack(ref, sd, cfg)
-        m_gpu = reference.mask_from_stack(out_gpu, sd, cfg)
+        mask_cpu_s = time.perf_counter() - t5
+        # the product path: HIP stack, then the HIP mask head
+        m_gpu = mask_of(out_gpu)
         snr_mask = signals.snr_db(m_ref.numpy(), m_gpu.numpy())
-        snr_alts = {p: signals.snr_db(m_ref.numpy(), reference.mask_from_stack(v[2], sd, cfg).numpy())
-                    for p, v in alts.items()}
+        snr_alts = {p: signals.snr_db(m_ref.numpy(), mask_of(v[2]).numpy()) for p, v in alts.items()}
+        result["mask_head"]["cpu_ms_per_chunk"] = round(mask_cpu_s * 1e3, 1)
+        result["mask_head"]["cpu_sample"] = f"oracle fp32 mask estimator on {threads} threads, one chunk"
+        # the head alone: HIP mask head on the fp32 stack output against the fp32 mask estimator
+        result["mask_head"]["head_snr_db_vs_fp32"] = round(signals.snr_db(m_ref.numpy(), mask_of(ref).numpy()), 2)
         result["cpu_baseline"] = {
             "value": round(1.0 / cpu_s, 5),
             "unit": "stack forwards/s",

@@ -19,7 +19,7 @@
 //   GEMM2(u-1): acc += W2(u-1) . tanh(tile u-1), its B operands straight from the tanh registers in
 //               accumulator order (W2 is packed with its k order permuted to match).
 // Stage 0 multiplies its W2 blocks (tile 0) by tanh(0) = 0 exactly; a last stage runs tanh and GEMM2 of
-// the last tile.  b1 is added with the tanh, b2 and the GLU in the epilogue.
+// the last tile.  b1 is added with the tanh; the GEMM2 accumulators start at b2; the GLU is the epilogue.
 #include "trf_device.h"
 
 namespace trf {
@@ -27,7 +27,7 @@ namespace trf {
 constexpr int kMaskWaves = kMaskFrames / 32;
 constexpr int kMaskStageBlocks = kMaskW1Blocks + 8 * kMaskPairs;  // LDS blocks of the largest stage
 constexpr float kMaskNormScale = 16.0f;                           // sqrt(dim) of the RMSNorm
-constexpr int kMaskPrefetch = 4;                                  // LDS operand reads ahead of their MFMA
+constexpr int kBufferRsrcWord3 = 0x00020000;                      // gfx9 raw buffer descriptor, word 3
 
 // hi = f16(a), f16(b) and lo = f16(a - hi), f16(b - hi) as packed pairs.
 __device__ __forceinline__ void split_f16(float a, float b, uint32_t& hi, uint32_t& lo) {
@@ -43,44 +43,43 @@ __device__ __forceinline__ float tanh_f32(float x) {
   return fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
 }
 
-// The MFMA sequence of a stage: N1 GEMM1 MFMAs then N2 GEMM2 MFMAs, with their LDS operand blocks.
-//   GEMM1 MFMA k (k < N1): k-step s = k / T, term = k % T (0: hi.hi, 1: W hi . x lo, 2: W lo . x hi),
-//     accumulator chain (s + term) & 1, so consecutive MFMAs alternate chains.
-//   GEMM2 MFMA m = k - N1: split: m = 6 (2i + t) + 2 term + ag; fp16: m = 2 (2i + t) + ag, for output pair
-//     i, hidden k-step t (units 16t..16t+15 of the tile) and a/g tile ag, so a and g chains alternate.
+// The work of a stage in units, each reading its LDS operand blocks once:
+//   unit k < 16: GEMM1 k-step s = k; split: blocks W1 hi(s), lo(s) and MFMAs hi.xh, hi.xl, lo.xh into
+//     accumulator chains s, s+1, s (mod 2), so that consecutive MFMAs alternate chains; fp16: hi(s) . xh.
+//   unit 16 + 2i + t: GEMM2 of output pair i, hidden k-step t (units 16t..16t+15 of the tile); split:
+//     blocks a hi, a lo, g hi, g lo and MFMAs a.hh, g.hh, a.hl, g.hl, a_lo.hh, g_lo.hh (a and g chains
+//     alternate); fp16: a.hh, g.hh.
 // LDS blocks of a stage: split = the packed tile's order (W1 blocks 0..31, W2 of pair i at 32 + 8i + ...);
 // fp16 = hi blocks only (W1 s at s, W2 of pair i, ag, t at 16 + 4i + 2ag + t).
 template <bool SPLIT, int NP>
 struct MaskOps {
-  static constexpr int T = SPLIT ? 3 : 1;
-  static constexpr int N1 = 16 * T;
-  static constexpr int N2 = 4 * NP * T;
+  static constexpr int U1 = 16;               // GEMM1 units
+  static constexpr int U = U1 + 2 * NP;       // all units of a stage
+  static constexpr int R = SPLIT ? 4 : 2;     // LDS reads of a GEMM2 unit (a GEMM1 unit reads R / 2)
   static constexpr int W1B = SPLIT ? kMaskW1Blocks : kMaskW1Blocks / 2;  // LDS blocks of W1
   static constexpr int NB = W1B + (SPLIT ? 8 : 4) * NP;                  // LDS blocks of a stage
-  __host__ __device__ static constexpr int step(int k) { return k / T; }
-  __host__ __device__ static constexpr int term(int k) { return k < N1 ? k % T : ((k - N1) % (2 * T)) / 2; }
-  __host__ __device__ static constexpr int chain(int k) { return (step(k) + term(k)) & 1; }
-  __host__ __device__ static constexpr int pair(int k) { return (k - N1) / (4 * T); }
-  __host__ __device__ static constexpr int kstep2(int k) { return ((k - N1) / (2 * T)) & 1; }
-  __host__ __device__ static constexpr int ag(int k) { return (k - N1) & 1; }
-  __host__ __device__ static constexpr int block(int k) {
-    if (k < N1) return SPLIT ? 2 * step(k) + (term(k) == 2) : step(k);
-    return SPLIT ? W1B + 8 * pair(k) + 4 * ag(k) + 2 * kstep2(k) + (term(k) == 2)
-                 : W1B + 4 * pair(k) + 2 * ag(k) + kstep2(k);
+  __host__ __device__ static constexpr int reads(int k) { return k < U1 ? R / 2 : R; }
+  // LDS block of read r of unit k (GEMM2 reads: split a hi, a lo, g hi, g lo; fp16 a, g).
+  __host__ __device__ static constexpr int block(int k, int r) {
+    if (k < U1) return SPLIT ? 2 * k + r : k;
+    const int i = (k - U1) >> 1, t = (k - U1) & 1;
+    return SPLIT ? W1B + 8 * i + 4 * (r >> 1) + 2 * t + (r & 1) : W1B + 4 * i + 2 * r + t;
   }
 };
 
 // One stage.  LAST: tanh and GEMM2 of the last hidden tile only.  Otherwise: pre := tile u-1 (+ b1),
-// tanh(pre) into the GEMM2 B operands between GEMM1(u)'s MFMAs, then GEMM2(u-1); b1 of tile u is loaded
-// for the next stage.
-template <bool SPLIT, int NP, bool LAST>
+// tanh(pre) into the GEMM2 B operands, one value after each GEMM1 unit, then GEMM2(u-1); b1 of tile u is
+// loaded for the next stage, and dma(q) issues this wave's q-th direct-to-LDS block of the next stage
+// after unit q.  (Issued all at once, the next stage's 40-80 KB per workgroup outrun what a CU keeps in
+// flight and the wave stalls in issue before its MFMAs; spread over the first units, they stream under
+// them and land before the stage ends.)  Each unit's operand blocks are read one unit ahead.
+template <bool SPLIT, int NP, bool LAST, typename Dma>
 __device__ __forceinline__ void mask_stage(const u32x4* L, int u, const float* b1, const u32x4 (&xh)[16],
                                            const u32x4 (&xl)[16], f32x16& hA, f32x16& hB, f32x4 (&b1v)[4],
-                                           f32x16 (&acc)[2 * NP], int lane, int hh) {
+                                           f32x16 (&acc)[2 * NP], int lane, int hh, Dma&& dma) {
   using O = MaskOps<SPLIT, NP>;
-  constexpr int K0 = LAST ? O::N1 : 0;  // first MFMA of the stage in the sequence
-  constexpr int N = O::N1 + O::N2;
-  constexpr int D = kMaskPrefetch;
+  constexpr int K0 = LAST ? O::U1 : 0;  // first unit of the stage
+  static_assert(O::NB / kMaskWaves <= O::U, "one DMA block per unit");
   float pre[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) pre[r] = hA[r] + hB[r] + b1v[r >> 2][r & 3];
@@ -103,34 +102,47 @@ __device__ __forceinline__ void mask_stage(const u32x4* L, int u, const float* b
 #pragma unroll
     for (int s = 0; s < 16; ++s) tanh_value(s);
   }
-  u32x4 a[D];
+  u32x4 cur[O::R], nxt[O::R];
 #pragma unroll
-  for (int i = 0; i < D; ++i) a[i] = L[O::block(K0 + i) * 64 + lane];
-  // MFMA k of the sequence, operand a[(k - K0) % D]; then the read kMaskPrefetch ahead.  (Two loops, so
-  // that each stays under the compiler's full-unroll size limit.)
-  auto op = [&](int k) {
-    const int i = k - K0;
-    if (k < O::N1) {
-      const int s = O::step(k);
-      const u32x4 b = (SPLIT && O::term(k) == 1) ? xl[s] : xh[s];
-      if (O::chain(k))
-        hB = mfma32h(a[i % D], b, k < 2 ? zero16() : hB);
-      else
-        hA = mfma32h(a[i % D], b, k < 2 ? zero16() : hA);
-    } else {
-      const int t = O::kstep2(k);
-      const u32x4 b = (SPLIT && O::term(k) == 1) ? hbl[t] : hbh[t];
-      f32x16& c = acc[2 * O::pair(k) + O::ag(k)];
-      c = mfma32h(a[i % D], b, c);
+  for (int r = 0; r < O::reads(K0); ++r) nxt[r] = L[O::block(K0, r) * 64 + lane];
+  auto unit = [&](int k) {
+#pragma unroll
+    for (int r = 0; r < O::R; ++r) cur[r] = nxt[r];
+    if (k + 1 < O::U) {
+#pragma unroll
+      for (int r = 0; r < O::reads(k + 1); ++r) nxt[r] = L[O::block(k + 1, r) * 64 + lane];
     }
-    if (k + D < N) a[i % D] = L[O::block(k + D) * 64 + lane];
-    if (!LAST && k < O::N1 && O::term(k) == O::T - 1) tanh_value(O::step(k));
+    if (k < O::U1) {
+      f32x16& c0 = (k & 1) ? hB : hA;  // chain of the hi.hi and lo.hi products
+      f32x16& c1 = (k & 1) ? hA : hB;  // chain of hi.lo
+      // First products of the chains start from zero: hA at k-step 0; hB at k-step 0 (split, its hi.lo)
+      // or 1 (fp16).
+      c0 = mfma32h(cur[0], xh[k], (k == 0 || (!SPLIT && k == 1)) ? zero16() : c0);
+      if (SPLIT) {
+        c1 = mfma32h(cur[0], xl[k], k == 0 ? zero16() : c1);
+        c0 = mfma32h(cur[1], xh[k], c0);
+      }
+      if (!LAST) tanh_value(k);
+    } else {
+      const int i = (k - O::U1) >> 1, t = (k - O::U1) & 1;
+      f32x16& a = acc[2 * i];
+      f32x16& g = acc[2 * i + 1];
+      a = mfma32h(cur[0], hbh[t], a);
+      g = mfma32h(cur[SPLIT ? 2 : 1], hbh[t], g);
+      if (SPLIT) {
+        a = mfma32h(cur[0], hbl[t], a);
+        g = mfma32h(cur[2], hbl[t], g);
+        a = mfma32h(cur[1], hbh[t], a);
+        g = mfma32h(cur[3], hbh[t], g);
+      }
+    }
+    if (!LAST && k < O::NB / kMaskWaves) dma(k);
     __builtin_amdgcn_sched_barrier(0);
   };
 #pragma unroll
-  for (int k = K0; k < O::N1; ++k) op(k);
+  for (int k = K0; k < O::U1; ++k) unit(k);
 #pragma unroll
-  for (int k = O::N1; k < N; ++k) op(k);
+  for (int k = O::U1; k < O::U; ++k) unit(k);
 }
 
 template <bool SPLIT, int NP>
@@ -146,25 +158,29 @@ __device__ __forceinline__ void mask_job(const MaskPlan& p, const float* __restr
   const int npairs = (din + 31) >> 5;
   const int tstride = (kMaskW1Blocks + 8 * npairs) * 64;  // u32x4 per hidden tile
   const int nht = p.hidden >> 5;
-  const u32x4* wb = reinterpret_cast<const u32x4*>(packed + size_t(p.wofs_kb[band]) * 1024);
   const float* b1 = reinterpret_cast<const float*>(packed + p.b1_off) + size_t(band) * p.hidden;
 
-  // Stage u's blocks into LDS buffer dst: W1 of tile u (none for u = nht) and W2 of tile max(u-1, 0),
-  // pairs p0..p0+NP-1; this wave takes every kMaskWaves-th block.
-  auto issue = [&](int u, u32x4* dst) {
-    const u32x4* t1 = wb + size_t(u) * tstride;
-    const u32x4* t2 = wb + size_t(u > 0 ? u - 1 : 0) * tstride + (kMaskW1Blocks + 8 * p0) * 64;
-    for (int b = wave + (u < nht ? 0 : O::W1B); b < O::NB; b += kMaskWaves) {
-      const u32x4* src = b < O::W1B ? t1 + (SPLIT ? b : 2 * b) * 64 : t2 + (SPLIT ? b - O::W1B : 2 * (b - O::W1B)) * 64;
-      lds_load_block(src, dst + b * 64, lane);
-    }
+  // Block q of this wave (block b = wave + kMaskWaves q) of stage u into LDS buffer dst: W1 of tile u (for
+  // u = nht tile nht-1 again, unused: no branch) and W2 of tile max(u-1, 0), pairs p0..p0+NP-1.  A buffer load over the band's weights:
+  // the block's offset is scalar and the lane offset one register for all blocks (reads past the band's
+  // weights would return zeros).
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(packed) + size_t(p.wofs_kb[band]) * 1024, 0, nht * tstride * 16, kBufferRsrcWord3);
+  const int voff = lane * 16;
+  auto issue = [&](int u, u32x4* dst, int q) {
+    const int b = wave + kMaskWaves * q;
+    const int blk = b < O::W1B ? (u < nht ? u : nht - 1) * (tstride / 64) + (SPLIT ? b : 2 * b)
+                               : (u > 0 ? u - 1 : 0) * (tstride / 64) + kMaskW1Blocks + 8 * p0 +
+                                     (SPLIT ? b - O::W1B : 2 * (b - O::W1B));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(dst + b * 64),
+                                             16, voff, blk * 1024, 0, 0);
   };
-
   const int n = tb * kMaskFrames + wave * 32 + j;
   // Lanes past the last frame work on a copy of the last frame (a column of their own) and store nothing.
   const bool valid = n < p.n_frames;
   const float* xr = X + (int64_t(valid ? n : p.n_frames - 1) * p.F + band) * kDim;
-  issue(0, lds0);
+#pragma unroll
+  for (int q = 0; q < O::NB / kMaskWaves; ++q) issue(0, lds0, q);
   // This lane's half of the frame's 256 features: k = 16s + 8hh + e, the B-operand order of k-step s.
   f32x4 xv[32];
 #pragma unroll
@@ -172,6 +188,24 @@ __device__ __forceinline__ void mask_job(const MaskPlan& p, const float* __restr
     xv[2 * s] = *reinterpret_cast<const f32x4*>(xr + 16 * s + 8 * hh);
     xv[2 * s + 1] = *reinterpret_cast<const f32x4*>(xr + 16 * s + 8 * hh + 4);
   }
+  // The GEMM2 accumulators start at b2: a tile of pair i at b2[c], its g tile at b2[pad + c] for the
+  // lane's columns c (every c < pad: the packed b2 is zero past din, so no guard is needed).
+  const float* b2 = reinterpret_cast<const float*>(packed + p.b2_off[band]);
+  const int pad = 32 * npairs;
+  f32x16 acc[2 * NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = 32 * (p0 + i) + 8 * g + 4 * hh;
+      const f32x4 ba = *reinterpret_cast<const f32x4*>(b2 + c);
+      const f32x4 bg = *reinterpret_cast<const f32x4*>(b2 + pad + c);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[2 * i][4 * g + r] = ba[r];
+        acc[2 * i + 1][4 * g + r] = bg[r];
+      }
+    }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 32; ++i)
@@ -195,26 +229,21 @@ __device__ __forceinline__ void mask_job(const MaskPlan& p, const float* __restr
   f32x4 b1v[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) b1v[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x16 acc[2 * NP];
-#pragma unroll
-  for (int i = 0; i < 2 * NP; ++i) acc[i] = zero16();
   // Stages go in pairs so that each one's LDS buffer is a compile-time constant (the compiler then tells
   // operand reads from the direct-to-LDS loads into the other buffer and does not wait for those).
 #pragma clang loop unroll(disable)
   for (int u = 0; u < nht; u += 2) {
     stage_barrier();
-    issue(u + 1, lds1);
-    mask_stage<SPLIT, NP, false>(lds0, u, b1, xh, xl, hA, hB, b1v, acc, lane, hh);
+    mask_stage<SPLIT, NP, false>(lds0, u, b1, xh, xl, hA, hB, b1v, acc, lane, hh,
+                                 [&](int q) { issue(u + 1, lds1, q); });
     stage_barrier();
-    issue(u + 2, lds0);
-    mask_stage<SPLIT, NP, false>(lds1, u + 1, b1, xh, xl, hA, hB, b1v, acc, lane, hh);
+    mask_stage<SPLIT, NP, false>(lds1, u + 1, b1, xh, xl, hA, hB, b1v, acc, lane, hh,
+                                 [&](int q) { issue(u + 2, lds0, q); });
   }
   stage_barrier();
-  mask_stage<SPLIT, NP, true>(lds0, nht, b1, xh, xl, hA, hB, b1v, acc, lane, hh);
+  mask_stage<SPLIT, NP, true>(lds0, nht, b1, xh, xl, hA, hB, b1v, acc, lane, hh, [](int) {});
 
   if (!valid) return;
-  const float* b2 = reinterpret_cast<const float*>(packed + p.b2_off[band]);
-  const int pad = 32 * npairs;
   float* mrow = mask + int64_t(n) * p.width + p.col[band];
 #pragma unroll
   for (int i = 0; i < NP; ++i)
@@ -222,12 +251,9 @@ __device__ __forceinline__ void mask_job(const MaskPlan& p, const float* __restr
     for (int g = 0; g < 4; ++g) {
       const int c = 32 * (p0 + i) + 8 * g + 4 * hh;  // mask columns c..c+3 of the band
       if (c >= din) continue;
-      const f32x4 ba = *reinterpret_cast<const f32x4*>(b2 + c);
-      const f32x4 bg = *reinterpret_cast<const f32x4*>(b2 + pad + c);
       f32x4 m;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        m[r] = (acc[2 * i][4 * g + r] + ba[r]) / (1.0f + __expf(-(acc[2 * i + 1][4 * g + r] + bg[r])));
+      for (int r = 0; r < 4; ++r) m[r] = acc[2 * i][4 * g + r] / (1.0f + __expf(-acc[2 * i + 1][4 * g + r]));
       *reinterpret_cast<f32x4*>(mrow + c) = m;
     }
 }
