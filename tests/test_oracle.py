@@ -260,3 +260,29 @@ def test_ff_fp16_between_bf16_and_fp32(tiny_sd):
     db = snr_db((ref - x.double()).numpy(), (yb.double() - x.double()).numpy())
     assert d16 >= db + 12.0, (d16, db)
     assert d16 >= 60.0
+
+
+def test_split_f16_parts():
+    g = torch.Generator().manual_seed(4)
+    v = torch.randn(4096, generator=g) * torch.logspace(-3, 3, 4096)
+    hi, lo = ok._split_f16(v)
+    assert torch.equal(hi, hi.half().double())  # hi is an fp16 value
+    assert torch.equal(lo, lo.half().double())
+    # hi + lo carries ~22 significant bits, down to lo's subnormal step 2^-24 (rounding error 2^-25)
+    err = ((hi + lo) - v.double()).abs()
+    assert bool((err <= 2.0**-21 * v.double().abs() + 2.0**-25).all())
+    big = v.abs() > 0.5
+    assert float((err[big] / v.double().abs()[big]).max()) < 2.0**-21
+    assert float(((hi - v.double()).abs() / v.double().abs())[big].max()) > 2.0**-13  # hi alone does not
+
+
+def test_mask_head_emulation_against_reference(tiny_sd):
+    cfg = weights.TINY_CFG
+    dims = reference.band_dims(cfg)
+    x = 3.0 * torch.randn(1, 40, len(dims), 256, generator=torch.Generator().manual_seed(9))
+    ref = reference.mask_from_stack(x.double(), {k: v.double() for k, v in tiny_sd.items()}, cfg)[0].numpy()
+    split = ok.mask_head(x[0], tiny_sd, dims, precision="split").numpy()
+    f16 = ok.mask_head(x[0], tiny_sd, dims, precision="fp16").numpy()
+    assert split.shape == f16.shape == ref.shape == (40, sum(dims))
+    assert snr_db(ref, split) >= 110.0
+    assert 60.0 <= snr_db(ref, f16) <= 80.0  # fp16 operands do round
