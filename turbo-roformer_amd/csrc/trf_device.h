@@ -68,8 +68,27 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // Weights are packed as 1 KB operand blocks (one MFMA A operand: 64 lanes x 16 B).  A workgroup
 // streams the blocks of one stage into LDS with direct global->LDS loads, double-buffered: while the
 // waves compute on stage s from one buffer, the blocks of stage s+1 land in the other.
+//
+// The direct loads are buffer loads with an LDS destination (buffer_load_dwordx4 ... lds).  The compiler
+// counts global_load_lds among the LDS operations, so after one it can only wait lgkmcnt(0) before an
+// LDS read; after buffer loads it keeps exact lgkmcnt(n) waits for reads issued ahead of their use.
+// Buffer loads are also bounds-checked against the resource's size (reads past it return zeros).
+constexpr int kBufferRsrcWord3 = 0x00020000;  // word 3 of a gfx9 raw buffer descriptor
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferRsrcWord3);
+}
+
+// 16 bytes per lane from byte offset voff of buffer r into LDS at lds_base + 16 * lane (lds_base
+// wave-uniform).
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, int voff, u32x4* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, 0, 0,
+                                           0);
+}
+
+// One operand block (src_block wave-uniform) into LDS.
 __device__ __forceinline__ void lds_load_block(const u32x4* __restrict__ src_block, u32x4* lds_block, int lane) {
-  __builtin_amdgcn_global_load_lds(src_block + lane, lds_block, 16, 0, 0);
+  buffer_load_lds16(buffer_rsrc(src_block, kTileBytes), lane * 16, lds_block);
 }
 
 // All of this thread's outstanding global loads (direct-to-LDS ones included) have landed, and every

@@ -394,27 +394,24 @@ __device__ __forceinline__ int chunk_swz(int R) { return (R & 7) ^ ((R >> 3) & 1
 // This wave's share of staging one 8 KB K tile into LDS, chunk-major like K itself: LDS block c
 // (64 rows x 16 B) holds features 8c..8c+7 of the tile's 64 keys, row R = key (R&32)|pi(R&31).  Wave w
 // stages chunks 2w and 2w+1, one 1 KB instruction each (64 consecutive rows of one chunk plane).
-__device__ __forceinline__ void stage_k_tile(const uint16_t* __restrict__ Kh, int kt, int Lpad, u32x4* lds_tile,
+__device__ __forceinline__ void stage_k_tile(__amdgpu_buffer_rsrc_t kres, int kt, int Lpad, u32x4* lds_tile,
                                              int wave, int lane) {
   const int key = (lane & 32) | key_perm(lane & 31);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int c = 2 * wave + i;
-    const uint16_t* src = Kh + (int64_t(c) * Lpad + kt * 64 + key) * 8;
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src), lds_tile + c * 64, 16, 0, 0);
+    buffer_load_lds16(kres, (c * Lpad + kt * 64 + key) * 16, lds_tile + c * 64);
   }
 }
 
 // This wave's share of staging one 8 KB V^T tile (64 rows x 8 chunks of 16 B) into LDS: rows
 // 16w..16w+15 (two instructions of 8 rows).  Row R holds head feature R.
-__device__ __forceinline__ void stage_v_tile(const uint16_t* __restrict__ Vh, int kt, int Lpad, u32x4* lds_tile,
+__device__ __forceinline__ void stage_v_tile(__amdgpu_buffer_rsrc_t vres, int kt, int Lpad, u32x4* lds_tile,
                                              int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int R = 16 * wave + 8 * i + (lane >> 3), pc = lane & 7;
-    const uint16_t* src = Vh + int64_t(R) * Lpad + kt * 64 + 8 * (pc ^ chunk_swz(R));
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src), lds_tile + (16 * wave + 8 * i) * 8, 16,
-                                     0, 0);
+    buffer_load_lds16(vres, (R * Lpad + kt * 64 + 8 * (pc ^ chunk_swz(R))) * 2, lds_tile + (16 * wave + 8 * i) * 8);
   }
 }
 
@@ -540,8 +537,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   const int sh = xcd + 8 * (slot / nqb), qblk = slot % nqb;
   const int s = sh >> 3, h = sh & 7;
   const uint16_t* Qh = Q + int64_t(sh) * Lpad * kHeadDim;
-  const uint16_t* Kh = K + int64_t(sh) * Lpad * kHeadDim;
-  const uint16_t* Vh = Vt + int64_t(sh) * kHeadDim * Lpad;
+  // K and V^T of this (sequence, head) as buffer resources for the direct-to-LDS tile loads.
+  const __amdgpu_buffer_rsrc_t Kh = buffer_rsrc(K + int64_t(sh) * Lpad * kHeadDim, Lpad * kHeadDim * 2);
+  const __amdgpu_buffer_rsrc_t Vh = buffer_rsrc(Vt + int64_t(sh) * kHeadDim * Lpad, Lpad * kHeadDim * 2);
   const int q0 = qblk * kAttBlockQ + wave * 32 * kAttQT;
   const bool active = q0 < L;  // idle waves still stage tiles and meet every barrier
 

@@ -27,7 +27,6 @@ namespace trf {
 constexpr int kMaskWaves = kMaskFrames / 32;
 constexpr int kMaskStageBlocks = kMaskW1Blocks + 8 * kMaskPairs;  // LDS blocks of the largest stage
 constexpr float kMaskNormScale = 16.0f;                           // sqrt(dim) of the RMSNorm
-constexpr int kBufferRsrcWord3 = 0x00020000;                      // gfx9 raw buffer descriptor, word 3
 
 // hi = f16(a), f16(b) and lo = f16(a - hi), f16(b - hi) as packed pairs.
 __device__ __forceinline__ void split_f16(float a, float b, uint32_t& hi, uint32_t& lo) {
@@ -164,16 +163,15 @@ __device__ __forceinline__ void mask_job(const MaskPlan& p, const float* __restr
   // u = nht tile nht-1 again, unused: no branch) and W2 of tile max(u-1, 0), pairs p0..p0+NP-1.  A buffer load over the band's weights:
   // the block's offset is scalar and the lane offset one register for all blocks (reads past the band's
   // weights would return zeros).
-  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(packed) + size_t(p.wofs_kb[band]) * 1024, 0, nht * tstride * 16, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(packed + size_t(p.wofs_kb[band]) * 1024, nht * tstride * 16);
   const int voff = lane * 16;
   auto issue = [&](int u, u32x4* dst, int q) {
     const int b = wave + kMaskWaves * q;
     const int blk = b < O::W1B ? (u < nht ? u : nht - 1) * (tstride / 64) + (SPLIT ? b : 2 * b)
                                : (u > 0 ? u - 1 : 0) * (tstride / 64) + kMaskW1Blocks + 8 * p0 +
                                      (SPLIT ? b - O::W1B : 2 * (b - O::W1B));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(dst + b * 64),
-                                             16, voff, blk * 1024, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(dst + b * 64), 16,
+                                             voff, blk * 1024, 0, 0);
   };
   const int n = tb * kMaskFrames + wave * 32 + j;
   // Lanes past the last frame work on a copy of the last frame (a column of their own) and store nothing.
