@@ -13,9 +13,12 @@ chunk, whose output also gives the mask SNR of the GPU path.
 The mask head after the stack (final norm + 62 band MLPs + GLU, one HIP kernel) is timed on the chunk's
 stack output beside it, with its own CPU time (the oracle's fp32 mask estimator) and accuracy.
 
-It also separates a synthetic 4:12 song end to end (29 chunks in one batched stack forward and one
-mask-head launch on the GPU, host STFT / band split / iSTFT in PyTorch on the GPU, overlap-add on the CPU)
-and reports its real-time factor.
+The band split before the stack (62 band RMSNorms + Linears, one HIP kernel) produces the chunk's tokens on
+the GPU and is timed the same way.
+
+It also separates a synthetic 4:12 song end to end (for the 29 chunks: one band-split launch, one batched
+stack forward and one mask-head launch on the GPU, STFT / iSTFT in PyTorch on the GPU, overlap-add on the
+CPU) and reports its real-time factor.
 
     python bench.py [--steps K] [--warmup W] [--precision ff_fp16|ff_split|bf16] [--no-cpu] [--no-song]
 """
@@ -107,6 +110,7 @@ def main() -> int:
         return 2
 
     from turbo_roformer_amd import _hip, signals, weights
+    from turbo_roformer_amd.band_split import HipBandSplit
     from turbo_roformer_amd.host import HostPath
     from turbo_roformer_amd.stack import HipStack
 
@@ -114,9 +118,27 @@ def main() -> int:
     sd = weights.init_state_dict(cfg, seed=a.seed, init="default", perturb=True)
     host = HostPath(sd, cfg, "cpu")
     raw = torch.from_numpy(signals.noise_mix(SAMPLES, seed=a.seed))[None]
-    X0 = host.band_split(host.spectrogram(raw))  # (1, T, F, 256) fp32
+    feats = host.spectrogram(raw)  # (1, T, bins * 2 * 2) fp32
+    t_bs = time.perf_counter()
+    X0 = host.band_split(feats)  # (1, T, F, 256) fp32, torch on the host
+    band_cpu_s = time.perf_counter() - t_bs
     _, T, F, _ = X0.shape
-    Xd0 = X0.reshape(-1, 256).contiguous().cuda()
+    # the step before the stack on the GPU: band split of the chunk's features into the stack's tokens
+    bsplit = HipBandSplit(sd, cfg, "cuda")
+    fd = feats.reshape(T, -1).contiguous().cuda()
+    Xd0 = bsplit(fd)
+    for _ in range(3):
+        bsplit(fd, out=Xd0)
+    torch.cuda.synchronize()
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record()
+    for _ in range(20):
+        bsplit(fd, out=Xd0)
+    b1.record()
+    torch.cuda.synchronize()
+    band_ms = b0.elapsed_time(b1) / 20
+    band_snr = signals.snr_db(X0.reshape(-1, 256).numpy(), Xd0.cpu().numpy())
+    del fd
 
     if a.copy_calibration:
         src = torch.ones(COPY_CALIBRATION_BYTES // 4, device="cuda")
@@ -226,11 +248,14 @@ def main() -> int:
         "precision": a.precision,
         "other_precisions": {p: {"ms_per_step": round(v[0], 4), "value": round(1e3 / v[0], 3)} for p, v in alts.items()},
         "mask_head": result_mask,
+        "band_split": {"kernel": "band split (62 band RMSNorm + Linear, fp32 MFMA)", "ms_per_chunk": round(band_ms, 4),
+                       "torch_cpu_ms_per_chunk": round(band_cpu_s * 1e3, 1),
+                       "snr_db_vs_torch_fp32": round(band_snr, 2)},
     }
 
     if not a.no_song:
-        # whole synthetic 4:12 song: 29 chunks of 17 s at overlap 2, one batched stack forward, host STFT,
-        # band split and iSTFT in PyTorch and one mask-head launch on the same GPU, Hamming overlap-add on the CPU
+        # whole synthetic 4:12 song: 29 chunks of 17 s at overlap 2; band split, one batched stack forward and
+        # the mask head on the kernels, STFT and iSTFT in PyTorch on the same GPU, Hamming overlap-add on the CPU
         from turbo_roformer_amd.separator import Separator
 
         sep = Separator(sd, cfg, T, "cuda", precision=a.precision)

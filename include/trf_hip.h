@@ -4,7 +4,8 @@
  * The library replaces the seven AVX512-BF16 torch ops of LoggeL/turbo-roformer
  * (src/turbo_roformer/csrc/kernels.cpp:644-652) and the stack loop that calls them
  * (FastBSRoformer._transformer_cpp, src/turbo_roformer/fast.py:269-341) with HIP
- * kernels, and the mask head that follows the stack (FastBSRoformer._mask, fast.py:349-360).
+ * kernels, and the steps either side of it: the band split that feeds the stack and the mask head
+ * that follows it (fast.py:377-387).
  * Every entry point takes plain device pointers, sizes and a HIP stream;
  * no torch type appears in a signature.  The library allocates no memory and keeps
  * no state beyond a thread-local error string: the caller owns every buffer.
@@ -40,7 +41,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 3
+#define TRF_ABI_VERSION 4
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -205,6 +206,34 @@ int trf_attn_block(float* X, int32_t batch, int32_t T, int32_t F, const void* pa
  * model.py:142), with the FF GEMMs in the given trf_precision. */
 int trf_ff_block(float* X, int32_t batch, int32_t T, int32_t F, const void* packed_layer,
                  int32_t precision, void* workspace, size_t workspace_bytes, trf_stream_t stream);
+
+/* ---------------------------------------------------------------- band split
+ * The step before the stack: per band f of width dins[f] (2 * frequencies * channels), the RMSNorm
+ * of the frame's dins[f] spectral features and a Linear dins[f] -> 256 (BandSplit, model.py:147-155;
+ * called at fast.py:377-380), written as the stack's tokens X [n_frames * n_bands][256] fp32 (token
+ * n * n_bands + f).  The features are the reference's per-frame layout feats [n_frames][sum(dins)]
+ * fp32, (bin, channel, re/im) order (fast.py:372-376), band f at columns sum(dins[:f]) .. + dins[f].
+ * Arithmetic is fp32 (fp32 MFMA).  Limits: 1 <= n_bands <= 64; each din a multiple of 4 in
+ * [4, 16384]. */
+
+/* One band's plain fp32 weights, device pointers: band_split.to_features.<f>.1.weight [256][din],
+ * .1.bias [256] and the RMSNorm gain .0.gamma [din]. */
+typedef struct trf_band_split_src {
+  const float* w;
+  const float* b;
+  const float* gamma;
+} trf_band_split_src;
+
+/* Bytes of the packed band split (0 if the arguments are out of the limits above). */
+size_t trf_band_split_packed_bytes(const int32_t* dins, int32_t n_bands);
+
+/* Pack the bands (bands, dins: host arrays of n_bands) into packed (device, 16-byte aligned). */
+int trf_pack_band_split(const trf_band_split_src* bands, const int32_t* dins, int32_t n_bands, void* packed,
+                        trf_stream_t stream);
+
+/* X [n_frames * n_bands][256] from feats [n_frames][sum(dins)]; n_frames = 0 does nothing. */
+int trf_band_split(const float* feats, int32_t n_frames, int32_t n_bands, const int32_t* dins,
+                   const void* packed, float* X, trf_stream_t stream);
 
 /* ---------------------------------------------------------------- mask head
  * The step after the stack: final RMSNorm and, per band f of width dins[f] (its mask columns:

@@ -99,3 +99,21 @@ def test_mask_head_argument_errors_need_no_device(lib):
     assert lib.trf_mask_head(None, 0, 3, d, 1024, None, 0, None, None) == 0  # nothing to do
     assert lib.trf_pack_mask_head(None, d, 3, 1024, p, p, None) == 1
     assert b"bands" in lib.trf_last_error()
+
+
+def test_band_split_packed_bytes_and_errors(lib):
+    from turbo_roformer_amd import weights
+
+    dims = weights.band_dims(weights.RESURRECTION_CFG)
+    # fp32 W' as (din / 2) k-pairs x 8 tiles x 64 lanes (= 256 x din floats) plus the bias per band
+    assert lib.trf_band_split_packed_bytes(_dins(*dims), len(dims)) == 4 * 256 * (sum(dims) + len(dims))
+    p = ctypes.c_void_p(256)
+    assert lib.trf_band_split_packed_bytes(_dins(8, 18), 2) == 0
+    assert b"dins[1]" in lib.trf_last_error()
+    assert lib.trf_band_split_packed_bytes(_dins(8), 65) == 0
+    assert b"n_bands" in lib.trf_last_error()
+    assert lib.trf_band_split(p, -1, 1, _dins(8), p, p, None) == 1
+    assert lib.trf_band_split(p, 4, 1, _dins(8), None, p, None) == 1
+    assert b"packed must not be NULL" in lib.trf_last_error()
+    assert lib.trf_band_split(None, 0, 1, _dins(8), None, None, None) == 0  # nothing to do
+    assert lib.trf_pack_band_split(None, _dins(8), 1, p, None) == 1

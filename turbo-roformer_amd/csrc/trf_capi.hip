@@ -1,6 +1,7 @@
-// C ABI of the stack and the mask head (declared in include/trf_hip.h): argument checks, workspace and
-// packed layouts, the 24-sub-layer driver and the mask-head launch plan.  Host code only; the kernels
-// live in trf_kernels.hip and trf_mask.hip.
+// C ABI of the stack, the band split before it and the mask head after it (declared in include/trf_hip.h):
+// argument checks, workspace and packed layouts, the 24-sub-layer driver and the launch plans.  Host code
+// only; the kernels live in trf_kernels.hip, trf_band_split.hip and trf_mask.hip.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -184,8 +185,8 @@ int mask_njobs(int din) { return (mask_npairs(din) + trf::kMaskPairs - 1) / trf:
 
 int mask_layout(const int32_t* dins, int32_t n_bands, int32_t hidden, MaskLayout& L) {
   if (!dins) return fail(TRF_ERR_ARG, "dins must not be NULL");
-  if (n_bands < 1 || n_bands > trf::kMaskMaxBands)
-    return fail(TRF_ERR_ARG, "n_bands must be in [1, %d], got %d", trf::kMaskMaxBands, n_bands);
+  if (n_bands < 1 || n_bands > trf::kMaxBands)
+    return fail(TRF_ERR_ARG, "n_bands must be in [1, %d], got %d", trf::kMaxBands, n_bands);
   if (hidden < 64 || hidden > 8192 || hidden % 64)
     return fail(TRF_ERR_ARG, "hidden must be a multiple of 64 in [64, 8192], got %d", hidden);
   L = MaskLayout{};
@@ -237,7 +238,7 @@ unsigned mask_plan(const MaskLayout& L, int32_t n_frames, trf::MaskPlan& p) {
     p.wofs_kb[f] = uint32_t(L.wofs[f] / 1024);
     p.b2_off[f] = uint32_t(L.b2_off[f]);
     p.col[f] = uint32_t(col);
-    p.din[f] = uint16_t(L.din[f]);
+    p.din[f] = uint32_t(L.din[f]);
     col += L.din[f];
     const int np = mask_npairs(L.din[f]), nj = mask_njobs(L.din[f]);
     for (int q = 0, p0 = 0; q < nj; ++q) {
@@ -265,6 +266,24 @@ unsigned mask_plan(const MaskLayout& L, int32_t n_frames, trf::MaskPlan& p) {
   }
   p.xcd_start[trf::kXcds] = uint32_t(k);
   return unsigned(size_t(trf::kXcds) * most * p.ntb);
+}
+
+// ---------------------------------------------------------------- band split
+// Packed band split: per band (din / 2) * 8 * 64 fp32 A operands and the bias [256]; offsets in floats.
+int band_layout(const int32_t* dins, int32_t n_bands, std::vector<size_t>& wofs, size_t& total) {
+  if (!dins) return fail(TRF_ERR_ARG, "dins must not be NULL");
+  if (n_bands < 1 || n_bands > trf::kMaxBands)
+    return fail(TRF_ERR_ARG, "n_bands must be in [1, %d], got %d", trf::kMaxBands, n_bands);
+  wofs.clear();
+  total = 0;
+  for (int f = 0; f < n_bands; ++f) {
+    const int d = dins[f];
+    if (d < 4 || d > 16384 || d % 4)
+      return fail(TRF_ERR_ARG, "dins[%d] = %d: band widths must be multiples of 4 in [4, 16384]", f, d);
+    wofs.push_back(total);
+    total += size_t(d / 2) * 8 * 64 + trf::kDim;
+  }
+  return TRF_OK;
 }
 
 }  // namespace
@@ -482,6 +501,64 @@ int trf_mask_head(const float* X, int32_t n_frames, int32_t n_bands, const int32
   const unsigned grid = mask_plan(L, n_frames, plan);
   trf::launch_mask_head(X, static_cast<const uint8_t*>(packed), mask, plan, grid, precision, as_hip(stream));
   return check_launch("mask_head");
+}
+
+size_t trf_band_split_packed_bytes(const int32_t* dins, int32_t n_bands) {
+  std::vector<size_t> wofs;
+  size_t total;
+  if (band_layout(dins, n_bands, wofs, total)) return 0;
+  return total * 4;
+}
+
+int trf_pack_band_split(const trf_band_split_src* bands, const int32_t* dins, int32_t n_bands, void* packed,
+                        trf_stream_t stream) {
+  std::vector<size_t> wofs;
+  size_t total;
+  if (int rc = band_layout(dins, n_bands, wofs, total)) return rc;
+  if (!bands) return fail(TRF_ERR_ARG, "bands must not be NULL");
+  TRF_REQUIRE(packed, "packed");
+  for (int f = 0; f < n_bands; ++f)
+    if (!bands[f].w || !bands[f].b || !bands[f].gamma) return fail(TRF_ERR_ARG, "bands[%d] has a NULL pointer", f);
+  float* d = static_cast<float*>(packed);
+  for (int f = 0; f < n_bands; ++f) {
+    trf::launch_pack_band_split(bands[f].w, bands[f].b, bands[f].gamma, dins[f], sqrtf(float(dins[f])), d + wofs[f],
+                                as_hip(stream));
+    if (int rc = check_launch("pack_band_split")) return rc;
+  }
+  return TRF_OK;
+}
+
+int trf_band_split(const float* feats, int32_t n_frames, int32_t n_bands, const int32_t* dins, const void* packed,
+                   float* X, trf_stream_t stream) {
+  std::vector<size_t> wofs;
+  size_t total;
+  if (int rc = band_layout(dins, n_bands, wofs, total)) return rc;
+  if (n_frames < 0) return fail(TRF_ERR_ARG, "n_frames must be >= 0, got %d", n_frames);
+  if (int64_t(n_frames) * n_bands >= (int64_t(1) << 31))
+    return fail(TRF_ERR_ARG, "n_frames * n_bands = %lld tokens is too large", (long long)n_frames * n_bands);
+  if (n_frames == 0) return TRF_OK;
+  TRF_REQUIRE(feats, "feats");
+  TRF_REQUIRE(packed, "packed");
+  TRF_REQUIRE(X, "X");
+  trf::BandPlan plan{};
+  plan.n_bands = n_bands;
+  plan.n_frames = n_frames;
+  plan.ngroups = (n_frames + trf::kBandFrames - 1) / trf::kBandFrames;
+  int col = 0;
+  std::vector<int> order(n_bands);
+  for (int f = 0; f < n_bands; ++f) {
+    plan.col[f] = uint32_t(col);
+    plan.wofs[f] = uint32_t(wofs[f]);
+    plan.din[f] = uint32_t(dins[f]);
+    col += dins[f];
+    order[f] = f;
+  }
+  plan.width = col;
+  if (total >= (size_t(1) << 32)) return fail(TRF_ERR_ARG, "packed band split would exceed 16 GiB");
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return dins[a] > dins[b]; });  // widest first
+  for (int f = 0; f < n_bands; ++f) plan.order[f] = uint32_t(order[f]);
+  trf::launch_band_split(feats, static_cast<const float*>(packed), X, plan, as_hip(stream));
+  return check_launch("band_split");
 }
 
 }  // extern "C"

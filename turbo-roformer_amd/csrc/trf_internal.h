@@ -102,7 +102,7 @@ void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, int ff_p
 // "g" tile rows din + 32i + r (zero where 32i + r >= din), so a lane holds both GLU operands of a column.
 // Tile j is (32 + 8 * npairs) KB; the tiles of a band follow each other.  Then b1 [n_bands][hidden] and,
 // per band, b2 as [a part: pad][g part: pad] (pad = 32 * npairs, zeros past din), all fp32.
-constexpr int kMaskMaxBands = 64;
+constexpr int kMaxBands = 64;
 constexpr int kMaskMaxJobs = 192;
 constexpr int kMaskPairs = 6;      // output pairs per job: the largest that fits the LDS stages
 constexpr int kMaskFrames = 128;   // frames per workgroup (4 waves x 32)
@@ -119,11 +119,34 @@ struct MaskPlan {
   uint32_t b1_off;                  // byte offset of b1 in the packed buffer
   uint32_t xcd_start[kXcds + 1];
   uint32_t job[kMaskMaxJobs];       // band | np << 8 | p0 << 16
-  uint32_t wofs_kb[kMaskMaxBands];  // first weight block of the band, in KB from the packed start
-  uint32_t b2_off[kMaskMaxBands];   // byte offset of the band's b2
-  uint32_t col[kMaskMaxBands];      // first mask column of the band
-  uint16_t din[kMaskMaxBands];
+  uint32_t wofs_kb[kMaxBands];      // first weight block of the band, in KB from the packed start
+  uint32_t b2_off[kMaxBands];       // byte offset of the band's b2
+  uint32_t col[kMaxBands];          // first mask column of the band
+  uint32_t din[kMaxBands];
 };
+
+// Plans go to the kernels by value and are indexed at run time (by band or job), so every array in them
+// has 32-bit elements: with 16- or 8-bit elements next to 32-bit ones the compiler shared the address
+// arithmetic of two arrays and issued scalar loads from bases that were not dword aligned, which read the
+// wrong words for odd indices.
+
+// ---------------------------------------------------------------- band split (trf_band_split.hip)
+// Per band f: RMSNorm of the frame's din_f features, Linear din_f -> kDim.  Packed weights of a band:
+// W' = W * gamma * sqrt(din) as fp32 A operands of v_mfma_f32_32x32x2_f32, [din/2 k-pairs][8 tiles][64
+// lanes] (lane l: output 32t + l%32, input 2p + l/32), then the bias [kDim].
+constexpr int kBandFrames = 32;  // frames per workgroup (4 waves, 2 output tiles each)
+
+struct BandPlan {
+  int32_t n_bands, n_frames, width, ngroups;  // ngroups = workgroups per band
+  uint32_t col[kMaxBands];                    // first feature column of the band
+  uint32_t wofs[kMaxBands];                   // first float of the band's packed weights
+  uint32_t din[kMaxBands];
+  uint32_t order[kMaxBands];                  // bands in launch order, widest first
+};
+
+void launch_pack_band_split(const float* w, const float* b, const float* gamma, int din, float sqrt_din, float* dst,
+                            hipStream_t st);
+void launch_band_split(const float* feats, const float* packed, float* X, const BandPlan& plan, hipStream_t st);
 
 // Pack one band: W1 [hidden][kDim] (times gamma [kDim] per input), W2 [2 din][hidden], fp32 device.
 void launch_pack_mask_band(const float* w1, const float* gamma, const float* b1, const float* w2, const float* b2,

@@ -21,7 +21,7 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
 MODE_TIME, MODE_FREQ = 0, 1
@@ -61,6 +61,12 @@ class TrfMaskBandSrc(ctypes.Structure):
     _fields_ = [("w1", ctypes.c_void_p), ("b1", ctypes.c_void_p), ("w2", ctypes.c_void_p), ("b2", ctypes.c_void_p)]
 
 
+class TrfBandSplitSrc(ctypes.Structure):
+    """``trf_band_split_src`` of trf_hip.h: device pointers to one band's RMSNorm gain and Linear."""
+
+    _fields_ = [("w", ctypes.c_void_p), ("b", ctypes.c_void_p), ("gamma", ctypes.c_void_p)]
+
+
 _P, _I32, _I64, _F, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 _SIGNATURES: dict[str, tuple] = {
     "trf_abi_version": (ctypes.c_int, []),
@@ -87,6 +93,11 @@ _SIGNATURES: dict[str, tuple] = {
     ),
     "trf_attn_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _P, _SZ, _P]),
     "trf_ff_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _SZ, _P]),
+    "trf_band_split_packed_bytes": (_SZ, [ctypes.POINTER(ctypes.c_int32), _I32]),
+    "trf_pack_band_split": (
+        ctypes.c_int, [ctypes.POINTER(TrfBandSplitSrc), ctypes.POINTER(ctypes.c_int32), _I32, _P, _P]
+    ),
+    "trf_band_split": (ctypes.c_int, [_P, _I32, _I32, ctypes.POINTER(ctypes.c_int32), _P, _P, _P]),
     "trf_mask_head_packed_bytes": (_SZ, [ctypes.POINTER(ctypes.c_int32), _I32, _I32]),
     "trf_pack_mask_head": (
         ctypes.c_int, [ctypes.POINTER(TrfMaskBandSrc), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P]
@@ -439,3 +450,41 @@ def mask_head(X: torch.Tensor, n_frames: int, dins, hidden: int, packed: torch.T
     _need(mask, "mask", torch.float32, (n_frames, int(sum(dins))))
     _check(lib.trf_mask_head(X.data_ptr(), n_frames, F, _dins(dins), hidden, packed.data_ptr(),
                              MASK_PRECISIONS[precision], mask.data_ptr(), _stream()))
+
+
+# ---------------------------------------------------------------------------------------------- band split
+
+
+def band_split_packed_bytes(dins) -> int:
+    """Bytes of the packed band split for band widths ``dins``."""
+    lib = load()
+    n = lib.trf_band_split_packed_bytes(_dins(dins), len(dins))
+    if n == 0:
+        _check(1)
+    return int(n)
+
+
+def pack_band_split(bands: list[tuple[torch.Tensor, ...]], dins, out: torch.Tensor) -> None:
+    """Pack per-band ``(w [256, din], b [256], gamma [din])`` fp32 device tensors into ``out`` (uint8,
+    band_split_packed_bytes())."""
+    lib = load()
+    if len(bands) != len(dins):
+        raise ValueError("bands and dins differ in length")
+    for i, ((w, b, g), d) in enumerate(zip(bands, dins)):
+        _need(w, f"w[{i}]", torch.float32, (DIM, d))
+        _need(b, f"b[{i}]", torch.float32, (DIM,))
+        _need(g, f"gamma[{i}]", torch.float32, (d,))
+    _need(out, "out", torch.uint8, (lib.trf_band_split_packed_bytes(_dins(dins), len(dins)),))
+    src = (TrfBandSplitSrc * len(bands))(*[TrfBandSplitSrc(*(t.data_ptr() for t in b)) for b in bands])
+    _check(lib.trf_pack_band_split(src, _dins(dins), len(dins), out.data_ptr(), _stream()))
+
+
+def band_split(feats: torch.Tensor, n_frames: int, dins, packed: torch.Tensor, X: torch.Tensor) -> None:
+    """X [n_frames * len(dins), 256] = per-band RMSNorm + Linear of feats [n_frames, sum(dins)] fp32
+    (model.py:147-155), in the stack's token order."""
+    lib = load()
+    F = len(dins)
+    _need(feats, "feats", torch.float32, (n_frames, int(sum(dins))))
+    _need(packed, "packed", torch.uint8, (lib.trf_band_split_packed_bytes(_dins(dins), F),))
+    _need(X, "X", torch.float32, (n_frames * F, DIM))
+    _check(lib.trf_band_split(feats.data_ptr(), n_frames, F, _dins(dins), packed.data_ptr(), X.data_ptr(), _stream()))

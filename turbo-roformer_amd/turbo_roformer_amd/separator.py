@@ -3,10 +3,10 @@
 Mirrors ``turbo_roformer.Separator.separate`` (src/turbo_roformer/separator.py:182-232): the mix is made
 stereo, short inputs are padded to whole hops, loud mixes are scaled to a 0.9 peak and back, and the song
 is cut into chunks of hop * (dim_t - 1) samples at ``overlap`` predictions per sample and recombined
-with a Hamming-windowed overlap-add.  The difference is where a chunk's forward runs: STFT, band split
-and iSTFT stay in PyTorch (``HostPath``, on the same device); the 24-sub-layer stack of a whole batch of
-chunks is one ``trf_stack_forward`` call and the mask head after it one ``trf_mask_head`` call on the
-gfx950 kernels.  There is no CPU fallback: if the HIP library or the GPU is missing, construction raises
+with a Hamming-windowed overlap-add.  The difference is where a chunk's forward runs: STFT and iSTFT
+stay in PyTorch (``HostPath``, on the same device); for a whole batch of chunks, the band split is one
+``trf_band_split`` launch, the 24-sub-layer stack one ``trf_stack_forward`` call and the mask head one
+``trf_mask_head`` launch on the gfx950 kernels, the tokens staying on the device throughout.  There is no CPU fallback: if the HIP library or the GPU is missing, construction raises
 ``HipUnavailable``.
 
 Out of scope here: audio files, resampling (the reference uses soxr, absent from this image) and
@@ -23,6 +23,7 @@ import torch
 
 from . import _hip
 from .chunking import chunk_starts, overlap_add, step_for
+from .band_split import HipBandSplit
 from .host import HostPath
 from .mask import HipMaskHead
 from .stack import HipStack
@@ -76,6 +77,7 @@ class Separator:
         self.chunk = self.hop * (int(dim_t) - 1)
         self.batch_chunks = int(batch_chunks)
         self.host = HostPath(state_dict, cfg, self.device)
+        self.band_split = HipBandSplit(state_dict, cfg, self.device)
         self.stack = HipStack(state_dict, self.device, precision)
         self.mask_head = HipMaskHead(state_dict, cfg, self.device, mask_precision)
 
@@ -88,9 +90,10 @@ class Separator:
     def forward_chunks(self, chunks: torch.Tensor) -> torch.Tensor:
         """(b, 2, C) chunks -> (b, 2, hop * (frames - 1)) instrumental predictions, b chunks batched."""
         raw = chunks.to(self.device, torch.float32)
-        X = self.host.band_split(self.host.spectrogram(raw))  # (b, T, F, 256)
-        b, T, F, d = X.shape
-        Xd = X.reshape(b * T * F, d).contiguous()
+        feats = self.host.spectrogram(raw)  # (b, T, bins * 2 * 2)
+        b, T = feats.shape[:2]
+        F = len(self.band_split.dims)
+        Xd = self.band_split(feats.contiguous())  # (b * T * F, 256)
         self.stack(Xd, b, T, F)
         mask = self.mask_head(Xd, b * T).view(b, T, -1)
         return self.host.apply(raw, mask)
