@@ -5,7 +5,7 @@
  * (src/turbo_roformer/csrc/kernels.cpp:644-652) and the stack loop that calls them
  * (FastBSRoformer._transformer_cpp, src/turbo_roformer/fast.py:269-341) with HIP
  * kernels, and the steps either side of it: the band split that feeds the stack and the mask head
- * that follows it (fast.py:377-387).
+ * that follows it (fast.py:377-387), plus the overlap-add that assembles a song from its chunks.
  * Every entry point takes plain device pointers, sizes and a HIP stream;
  * no torch type appears in a signature.  The library allocates no memory and keeps
  * no state beyond a thread-local error string: the caller owns every buffer.
@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 4
+#define TRF_ABI_VERSION 5
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -234,6 +234,21 @@ int trf_pack_band_split(const trf_band_split_src* bands, const int32_t* dins, in
 /* X [n_frames * n_bands][256] from feats [n_frames][sum(dins)]; n_frames = 0 does nothing. */
 int trf_band_split(const float* feats, int32_t n_frames, int32_t n_bands, const int32_t* dins,
                    const void* packed, float* X, trf_stream_t stream);
+
+/* ---------------------------------------------------------------- song assembly
+ * Hamming-windowed overlap-add of chunk predictions (the reference's overlap_add, chunking.py:39-61):
+ * for chunks in ascending order, acc[ch][s:s+L] += y[c][ch][:L] * window[:L] and wsum[s:s+L] += window[:L],
+ * each term with the reference's two fp32 roundings (product, then sum), so the sums are bitwise those of
+ * its loop; a song processed in several batches calls trf_overlap_add once per batch, in chunk order.
+ * y [n_chunks][2][y_stride] fp32; starts: device int64 [n_chunks], ascending, each chunk's first sample;
+ * window: device fp32 [>= L]; acc [2][n] and wsum [n]: device fp32, zeroed before the first batch. */
+int trf_overlap_add(const float* y, int32_t n_chunks, int64_t y_stride, int32_t L, const int64_t* starts,
+                    const float* window, int64_t n, float* acc, float* wsum, trf_stream_t stream);
+
+/* out [2][n] = acc / max(wsum, 1e-10) / gain, two correctly rounded divisions (out may be acc): the
+ * reference's normalisation by the summed window, then by the peak gain (separator.py:187-201). */
+int trf_overlap_finish(const float* acc, const float* wsum, int64_t n, float gain, float* out,
+                       trf_stream_t stream);
 
 /* ---------------------------------------------------------------- mask head
  * The step after the stack: final RMSNorm and, per band f of width dins[f] (its mask columns:

@@ -117,3 +117,15 @@ def test_band_split_packed_bytes_and_errors(lib):
     assert b"packed must not be NULL" in lib.trf_last_error()
     assert lib.trf_band_split(None, 0, 1, _dins(8), None, None, None) == 0  # nothing to do
     assert lib.trf_pack_band_split(None, _dins(8), 1, p, None) == 1
+
+
+def test_overlap_add_argument_errors_need_no_device(lib):
+    p = ctypes.c_void_p(256)
+    assert lib.trf_overlap_add(p, 3, 100, 0, p, p, 1000, p, p, None) == 1
+    assert b"L must be" in lib.trf_last_error()
+    assert lib.trf_overlap_add(p, 3, 100, 101, p, p, 1000, p, p, None) == 1
+    assert lib.trf_overlap_add(p, 3, 100, 50, None, p, 1000, p, p, None) == 1
+    assert lib.trf_overlap_add(None, 0, 100, 50, None, None, 1000, None, None, None) == 0  # nothing to do
+    assert lib.trf_overlap_finish(p, p, 1000, 0.0, p, None) == 1
+    assert b"gain" in lib.trf_last_error()
+    assert lib.trf_overlap_finish(None, None, 0, 1.0, None, None) == 0

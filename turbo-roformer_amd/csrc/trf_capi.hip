@@ -561,4 +561,26 @@ int trf_band_split(const float* feats, int32_t n_frames, int32_t n_bands, const 
   return check_launch("band_split");
 }
 
+int trf_overlap_add(const float* y, int32_t n_chunks, int64_t y_stride, int32_t L, const int64_t* starts,
+                    const float* window, int64_t n, float* acc, float* wsum, trf_stream_t stream) {
+  if (n_chunks < 0 || n < 0) return fail(TRF_ERR_ARG, "n_chunks and n must be >= 0 (got %d, %lld)", n_chunks, (long long)n);
+  if (n_chunks == 0 || n == 0) return TRF_OK;
+  if (L < 1 || int64_t(L) > y_stride)
+    return fail(TRF_ERR_ARG, "L must be in [1, y_stride] (got L = %d, y_stride = %lld)", L, (long long)y_stride);
+  if (2 * n >= (int64_t(1) << 31) * 256) return fail(TRF_ERR_ARG, "n = %lld samples is too large", (long long)n);
+  if (!y || !starts || !window || !acc || !wsum) return fail(TRF_ERR_ARG, "pointers must not be NULL");
+  trf::launch_overlap_add(y, n_chunks, y_stride, L, starts, window, n, acc, wsum, as_hip(stream));
+  return check_launch("overlap_add");
+}
+
+int trf_overlap_finish(const float* acc, const float* wsum, int64_t n, float gain, float* out, trf_stream_t stream) {
+  if (n < 0) return fail(TRF_ERR_ARG, "n must be >= 0, got %lld", (long long)n);
+  if (n == 0) return TRF_OK;
+  if (!(gain > 0.f)) return fail(TRF_ERR_ARG, "gain must be > 0");
+  if (2 * n >= (int64_t(1) << 31) * 256) return fail(TRF_ERR_ARG, "n = %lld samples is too large", (long long)n);
+  if (!acc || !wsum || !out) return fail(TRF_ERR_ARG, "pointers must not be NULL");
+  trf::launch_overlap_finish(acc, wsum, n, gain, out, as_hip(stream));
+  return check_launch("overlap_finish");
+}
+
 }  // extern "C"

@@ -148,6 +148,13 @@ void launch_pack_band_split(const float* w, const float* b, const float* gamma, 
                             hipStream_t st);
 void launch_band_split(const float* feats, const float* packed, float* X, const BandPlan& plan, hipStream_t st);
 
+// ---------------------------------------------------------------- song assembly (trf_song.hip)
+// acc [2][n] += the windowed chunk predictions y [nc][2][ystride] (first L samples) at starts[nc] (device,
+// ascending), wsum [n] += the window, in ascending chunk order; then out = acc / max(wsum, 1e-10) / gain.
+void launch_overlap_add(const float* y, int nc, int64_t ystride, int L, const int64_t* starts, const float* w,
+                        int64_t n, float* acc, float* wsum, hipStream_t st);
+void launch_overlap_finish(const float* acc, const float* wsum, int64_t n, float gain, float* out, hipStream_t st);
+
 // Pack one band: W1 [hidden][kDim] (times gamma [kDim] per input), W2 [2 din][hidden], fp32 device.
 void launch_pack_mask_band(const float* w1, const float* gamma, const float* b1, const float* w2, const float* b2,
                            int din, int hidden, uint8_t* wdst, float* b1dst, float* b2dst, hipStream_t st);

@@ -21,7 +21,7 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
 MODE_TIME, MODE_FREQ = 0, 1
@@ -98,6 +98,8 @@ _SIGNATURES: dict[str, tuple] = {
         ctypes.c_int, [ctypes.POINTER(TrfBandSplitSrc), ctypes.POINTER(ctypes.c_int32), _I32, _P, _P]
     ),
     "trf_band_split": (ctypes.c_int, [_P, _I32, _I32, ctypes.POINTER(ctypes.c_int32), _P, _P, _P]),
+    "trf_overlap_add": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P, _I64, _P, _P, _P]),
+    "trf_overlap_finish": (ctypes.c_int, [_P, _P, _I64, _F, _P, _P]),
     "trf_mask_head_packed_bytes": (_SZ, [ctypes.POINTER(ctypes.c_int32), _I32, _I32]),
     "trf_pack_mask_head": (
         ctypes.c_int, [ctypes.POINTER(TrfMaskBandSrc), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P]
@@ -488,3 +490,37 @@ def band_split(feats: torch.Tensor, n_frames: int, dins, packed: torch.Tensor, X
     _need(packed, "packed", torch.uint8, (lib.trf_band_split_packed_bytes(_dins(dins), F),))
     _need(X, "X", torch.float32, (n_frames * F, DIM))
     _check(lib.trf_band_split(feats.data_ptr(), n_frames, F, _dins(dins), packed.data_ptr(), X.data_ptr(), _stream()))
+
+
+# ---------------------------------------------------------------------------------------------- song assembly
+
+
+def overlap_add(y: torch.Tensor, L: int, starts: torch.Tensor, window: torch.Tensor, acc: torch.Tensor,
+                wsum: torch.Tensor) -> None:
+    """acc [2, n] += y[c, :, :L] * window[:L] at starts[c], wsum [n] += window[:L], chunk by chunk in
+    ascending order with the reference's fp32 roundings (chunking.py:39-61). y [nc, 2, Ly] fp32."""
+    lib = load()
+    nc = y.shape[0]
+    _need(y, "y", torch.float32)
+    if y.dim() != 3 or y.shape[1] != 2 or not 1 <= L <= y.shape[2]:
+        raise ValueError(f"y must be [chunks, 2, >= L], got {tuple(y.shape)} with L = {L}")
+    _need(starts, "starts", torch.int64, (nc,))
+    _need(window, "window", torch.float32)
+    if window.numel() < L:
+        raise ValueError("window is shorter than L")
+    _need(acc, "acc", torch.float32)
+    n = acc.shape[1]
+    _need(acc, "acc", torch.float32, (2, n))
+    _need(wsum, "wsum", torch.float32, (n,))
+    _check(lib.trf_overlap_add(y.data_ptr(), nc, y.shape[2], L, starts.data_ptr(), window.data_ptr(), n,
+                               acc.data_ptr(), wsum.data_ptr(), _stream()))
+
+
+def overlap_finish(acc: torch.Tensor, wsum: torch.Tensor, gain: float, out: torch.Tensor) -> None:
+    """out [2, n] = acc / max(wsum, 1e-10) / gain, correctly rounded (out may be acc)."""
+    lib = load()
+    n = acc.shape[1]
+    _need(acc, "acc", torch.float32, (2, n))
+    _need(wsum, "wsum", torch.float32, (n,))
+    _need(out, "out", torch.float32, (2, n))
+    _check(lib.trf_overlap_finish(acc.data_ptr(), wsum.data_ptr(), n, float(gain), out.data_ptr(), _stream()))

@@ -5,7 +5,9 @@ multiples of step = floor(chunk / overlap), the last chunk aligned to the end of
 symmetric Hamming window, and the weighted sum normalised by the summed weights.  They have to be the
 same, sample for sample, for a song to be split and recombined the way the reference does it.  What
 differs is the execution: ``overlap_add`` hands every chunk of the song to ``run`` in batches (one
-batched stack forward per batch) instead of one model call per chunk.
+batched stack forward per batch) instead of one model call per chunk, and ``overlap_add_device`` does
+the same with the song, the chunks, the predictions and the windowed sums on the GPU (``trf_overlap_add``,
+bitwise the same sums as the host loop).
 """
 
 from __future__ import annotations
@@ -78,3 +80,40 @@ def overlap_add(
             if progress is not None:
                 progress(done, len(starts))
     return out.div_(wsum.clamp_(min=1e-10))
+
+
+def overlap_add_device(
+    x: torch.Tensor,
+    chunk: int,
+    overlap: float,
+    run: Callable[[torch.Tensor], torch.Tensor],
+    batch: int = 0,
+    progress: Callable[[int, int], None] | None = None,
+    gain: float = 1.0,
+) -> torch.Tensor:
+    """``overlap_add`` with everything on the GPU: x (2, n) device -> (2, n) device, divided by ``gain``.
+
+    The chunks are cut on the device, ``run`` returns device predictions, and ``trf_overlap_add``
+    accumulates each batch in ascending chunk order with the host loop's fp32 roundings, so the result is
+    bitwise that of ``overlap_add`` followed by ``div_(gain)``.
+    """
+    from . import _hip
+
+    n = x.shape[1]
+    C = min(chunk, n)
+    starts = chunk_starts(n, C, step_for(C, overlap))
+    dev = x.device
+    w = torch.from_numpy(hamming(C)).to(dev)
+    acc = torch.zeros(2, n, dtype=torch.float32, device=dev)
+    wsum = torch.zeros(n, dtype=torch.float32, device=dev)
+    per = len(starts) if batch <= 0 else batch
+    for b0 in range(0, len(starts), per):
+        group = starts[b0 : b0 + per]
+        y = run(torch.stack([x[:, s : s + C] for s in group]).contiguous()).float().contiguous()
+        L = min(C, y.shape[-1])
+        _hip.overlap_add(y, L, torch.tensor(group, dtype=torch.int64, device=dev), w, acc, wsum)
+        if progress is not None:
+            for k in range(len(group)):
+                progress(b0 + k + 1, len(starts))
+    _hip.overlap_finish(acc, wsum, gain, acc)
+    return acc

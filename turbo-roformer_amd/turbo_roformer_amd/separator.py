@@ -3,7 +3,7 @@
 Mirrors ``turbo_roformer.Separator.separate`` (src/turbo_roformer/separator.py:182-232): the mix is made
 stereo, short inputs are padded to whole hops, loud mixes are scaled to a 0.9 peak and back, and the song
 is cut into chunks of hop * (dim_t - 1) samples at ``overlap`` predictions per sample and recombined
-with a Hamming-windowed overlap-add.  The difference is where a chunk's forward runs: STFT and iSTFT
+with a Hamming-windowed overlap-add (on the GPU, ``trf_overlap_add``: bitwise the reference's sums).  The difference is where a chunk's forward runs: STFT and iSTFT
 stay in PyTorch (``HostPath``, on the same device); for a whole batch of chunks, the band split is one
 ``trf_band_split`` launch, the 24-sub-layer stack one ``trf_stack_forward`` call and the mask head one
 ``trf_mask_head`` launch on the gfx950 kernels, the tokens staying on the device throughout.  There is no CPU fallback: if the HIP library or the GPU is missing, construction raises
@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import _hip
-from .chunking import chunk_starts, overlap_add, step_for
+from .chunking import chunk_starts, overlap_add_device, step_for
 from .band_split import HipBandSplit
 from .host import HostPath
 from .mask import HipMaskHead
@@ -115,7 +115,9 @@ class Separator:
         peak = float(np.abs(x).max())
         gain = PEAK / peak if peak > PEAK else 1.0
         xt = torch.from_numpy(np.ascontiguousarray(x * np.float32(gain) if gain != 1.0 else x))
-        inst = overlap_add(xt, self.chunk, overlap, self.forward_chunks, self.batch_chunks, progress)
-        if gain != 1.0:
-            inst.div_(gain)
-        return np.ascontiguousarray(inst.numpy()[:, :n0])
+        # the song goes to the GPU once; chunks, predictions and the windowed sums stay there
+        xd = xt.pin_memory().to(self.device, non_blocking=True)
+        inst = overlap_add_device(xd, self.chunk, overlap, self.forward_chunks, self.batch_chunks, progress, gain)
+        out = torch.empty(2, n0, dtype=torch.float32, pin_memory=True)
+        out.copy_(inst[:, :n0])
+        return out.numpy()
