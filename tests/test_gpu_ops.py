@@ -130,6 +130,34 @@ def test_attention(hip, layers, mode, batch, T, F):
     assert snr_db(exact.view(n, 512).numpy(), O.double().cpu().numpy()) >= 40.0
 
 
+def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers):
+    """Long sequences are swept with a fixed integer shift from the first 32 keys; a score far above it
+    overflows that sweep's sums, and the workgroup redoes the sweep with the raised-shift method.  Here the
+    32 queries 96..127 of every (sequence, head) are a multiple of key 700, so their scores on it are ~100
+    (base 2) above the rest: the result must still be the softmax."""
+    w, _ = layers[0]
+    mode, batch, T, F = 0, 1, 900, 2
+    n = batch * T * F
+    xn = ok.l2_rows(rand_x(n, 77)).to(torch.bfloat16)
+    Q, K, Vt, G = ok.qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], mode, batch, T, F)
+    K[:, :, :, 700, :] = 4.0
+    Q[:, :, :, 96:128, :] = 100.0 / (64 * 16.0) * 4.0  # q . k_700 = 64 * 4 * 0.39 = 100
+    Oref = ok.attention(Q, K, Vt, G, mode, batch, T, F)
+    O = torch.empty(n, 512, dtype=torch.bfloat16, device=DEV)
+    print("attention with a dominant key (guarded sweep)", flush=True)
+    _hip.attention(Q.to(DEV), K.to(DEV), Vt.to(DEV), G.to(DEV), O, mode, batch, T, F)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O.float()).all()
+    assert_bf16_close(Oref, O, "O", min_snr=48)
+    # the spiked queries attend to key 700 alone: O = gate * V[700]
+    idx = ok.token_index(mode, batch, T, F)  # [nseq, L] token of (sequence, position)
+    for s_ in range(idx.shape[0]):
+        tok = idx[s_, 100]
+        v700 = Vt[s_, :, :, 700].float()  # [8 heads, 64]
+        want = (G[tok].float()[:, None] * v700).reshape(512)
+        torch.testing.assert_close(O[tok].float().cpu(), want, rtol=1e-2, atol=1e-3)
+
+
 @pytest.mark.parametrize("which", [0, 1])
 @pytest.mark.parametrize("n", [1, 31, 1000, 4133])
 def test_gemm_res_norm(hip, layers, which, n):

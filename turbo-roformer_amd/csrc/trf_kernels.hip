@@ -13,6 +13,8 @@
 // for every GEMM/attention operand (kernels.cpp:30-33).
 #include "trf_device.h"
 
+#include <type_traits>
+
 namespace trf {
 
 // Token index of position p in sequence s (see the token-order contract in trf_hip.h).
@@ -375,8 +377,10 @@ __device__ __forceinline__ void attn_store(const f32x16 (&o)[2], int q, int L, i
 // (kernels.cpp:286-384) first finds the row max m, then forms e = 2^(s - m) (q carries the factor
 // log2(e), so scores are base-2 exponents), sums e in fp32, rounds P = e to bf16 unnormalised and
 // accumulates P.V; the epilogue scales by gate/sum.  Here one sweep over the keys does the same with an
-// integer shift c >= the running max in place of m (see kAttHeadroom): a power-of-two shift changes
-// neither the bf16 rounding of P nor the normalised result, and QK^T is computed once instead of twice.
+// integer shift c in place of m, fixed from the first 32 keys (see kAttHeadroomFast): a power-of-two
+// shift changes neither the bf16 rounding of P nor the normalised result, QK^T is computed once instead of
+// twice, and no max is taken after the first keys; a workgroup whose sums overflow redoes the sweep with
+// a shift raised as scores exceed it.
 // One workgroup = one (sequence, head) and 4 waves x 64 queries; each wave holds two 32-query column
 // tiles, so every K or V^T operand read from LDS feeds two MFMAs.  Tiles of 64 keys of K and V^T stream
 // through a ring of LDS buffers, loaded global->LDS directly (V^T with the XOR swizzle of its 16-byte
@@ -422,16 +426,23 @@ __device__ __forceinline__ void load_k_half(const u32x4* __restrict__ Kl, int kh
   for (int ks = 0; ks < 4; ++ks) ka[ks] = Kl[(2 * ks + hh) * 64 + 32 * kh + j];
 }
 
-// Softmax shift of the single pass.  Scores are base-2 exponents; the shift c of a query is an integer,
-// set from the first 32 keys and raised (never lowered) whenever a score exceeds it, to kAttHeadroom
-// above the running max.  Raising c by d scales the earlier probabilities, their sum and the P.V
-// accumulators by 2^-d: exact in fp32, and it commutes with the bf16 rounding of P.  With an integer
-// shift, P = bf16(2^(s-c)) = 2^-c bf16(2^s), so the normalised result does not depend on which integer
-// c is (up to the fp32 rounding of s - c): it is the non-online softmax of the reference with the
-// row max m replaced by an integer >= m, which only moves P's bf16 rounding by the factor 2^(m - ceil m).
-// The final c is within kAttHeadroom + 1 of the row max, so the largest probability stays >=
-// 2^-(kAttHeadroom+1) and nothing of the fp32/bf16 range is lost.
-constexpr float kAttHeadroom = 8.0f;
+// Softmax shift of the single pass.  Scores are base-2 exponents and the shift c of a query is an
+// integer.  With an integer shift, P = bf16(2^(s-c)) = 2^-c bf16(2^s), so the normalised result does not
+// depend on which integer c is (up to the fp32 rounding of s - c), as long as nothing over- or
+// underflows: it is the non-online softmax of the reference with the row max m replaced by an integer,
+// which only moves P's bf16 rounding by a factor 2^(m - c) that is a power of two times 2^(m - ceil m).
+//
+// The sweep therefore takes c once, from the first 32 keys, kAttHeadroomFast above their max, and
+// computes 2^(s - c) for every later key with no max at all.  Keys far below c underflow only past
+// 2^-126, i.e. more than ~94 below the first keys' max, where their weight is below fp32 resolution
+// anyway.  A key far above c (more than ~60 above the first keys' max) would overflow the sums: the
+// sweep checks every row's sum against kAttSafeSum (and O for finiteness) at the end, and if any row of
+// the workgroup fails, the workgroup redoes the sweep with the guarded shift: c raised (never lowered)
+// whenever a score exceeds it, to kAttHeadroom above the running max, with the earlier probabilities,
+// their sum and the P.V accumulators scaled by 2^-d (exact).
+constexpr float kAttHeadroom = 8.0f;       // guarded sweep
+constexpr float kAttHeadroomFast = 32.0f;  // fixed-shift sweep
+constexpr float kAttSafeSum = 1099511627776.0f;  // 2^40: fixed-shift sums at most this leave O finite
 
 // max of x over lanes l and l ^ 32: v_permlane32_swap exchanges the half-waves, so of its two results
 // one is x and the other the partner's value, in either order.
@@ -440,25 +451,28 @@ __device__ __forceinline__ float halfwave_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// One 32-key half of a tile for one 32-query column tile: S^T = K.Q^T accumulated onto -c, the shift
-// raised if a score exceeds it, then P = 2^(s - c) as two B operands and the fp32 sum.  FIRST (the
-// first half of tile 0, 32 valid keys) sets c from its own row max.
-template <bool FIRST, bool MASK>
+// One 32-key half of a tile for one 32-query column tile: S^T = K.Q^T accumulated onto -c, then
+// P = 2^(s - c) as two B operands and the fp32 sum.  FIRST (the first half of tile 0, 32 valid keys) sets c
+// from its own row max; SAFE (the guarded sweep) raises c when a score exceeds it.
+template <bool FIRST, bool MASK, bool SAFE>
 __device__ __forceinline__ void attn_half(const u32x4 (&ka)[4], const u32x4 (&qb)[4], int key0, int L, int hh,
                                           f32x16& negc, float& lsum, f32x16 (&o)[2], u32x4& p0, u32x4& p1) {
   f32x16 sacc = FIRST ? zero16() : negc;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[ks], sacc);
-  float hm = MASK ? block_max(sacc, key0, L, hh, -INFINITY) : block_max(sacc, 0, 32, hh, -INFINITY);
-  hm = halfwave_max(hm);  // the query's 32 keys sit in lanes j and j + 32
+  float hm = 0.f;
+  if (FIRST || SAFE) {
+    hm = MASK ? block_max(sacc, key0, L, hh, -INFINITY) : block_max(sacc, 0, 32, hh, -INFINITY);
+    hm = halfwave_max(hm);  // the query's 32 keys sit in lanes j and j + 32
+  }
   if (FIRST) {
-    const float c = ceilf(hm) + kAttHeadroom;
+    const float c = ceilf(hm) + (SAFE ? kAttHeadroom : kAttHeadroomFast);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       negc[r] = -c;
       sacc[r] -= c;
     }
-  } else if (__any(hm > 0.f)) {  // a score above the shift somewhere in the wave (rare)
+  } else if (SAFE && __any(hm > 0.f)) {  // a score above the shift somewhere in the wave (rare)
     const float d = hm > 0.f ? ceilf(hm) + kAttHeadroom : 0.f;
     const int di = int(d);
 #pragma unroll
@@ -476,7 +490,7 @@ __device__ __forceinline__ void attn_half(const u32x4 (&ka)[4], const u32x4 (&qb
 }
 
 // One 64-key tile: per 32-key half, scores and probabilities for both query tiles, then P.V.
-template <bool FIRST, bool MASK>
+template <bool FIRST, bool MASK, bool SAFE>
 __device__ __forceinline__ void attn_tile(const u32x4* __restrict__ Kl, const u32x4* __restrict__ Vl,
                                           const u32x4 (&qb)[kAttQT][4], int key0, int L, int j, int hh,
                                           f32x16 (&negc)[kAttQT], float (&lsum)[kAttQT], f32x16 (&o)[kAttQT][2]) {
@@ -488,9 +502,9 @@ __device__ __forceinline__ void attn_tile(const u32x4* __restrict__ Kl, const u3
 #pragma unroll
     for (int qt = 0; qt < kAttQT; ++qt) {
       if (FIRST && kh == 0)
-        attn_half<true, false>(ka, qb[qt], 0, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
+        attn_half<true, false, SAFE>(ka, qb[qt], 0, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
       else
-        attn_half<false, MASK>(ka, qb[qt], key0 + 32 * kh, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
+        attn_half<false, MASK, SAFE>(ka, qb[qt], key0 + 32 * kh, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
     }
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -555,39 +569,59 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   const int nkt = Lpad / 64;  // >= 2: this kernel runs for L > 64
   float lsum[kAttQT];
   f32x16 negc[kAttQT], o[kAttQT][2];
+  auto sweep = [&](auto safe_tag) {
+    constexpr bool SAFE = decltype(safe_tag)::value;
+#pragma unroll
+    for (int qt = 0; qt < kAttQT; ++qt) {
+      lsum[qt] = 0.f;
+      negc[qt] = o[qt][0] = o[qt][1] = zero16();
+    }
+#pragma unroll
+    for (int i = 0; i < kAttBufs - 1; ++i)
+      if (i < nkt) {
+        stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
+        stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
+      }
+    tile_barrier<4 * (kAttBufs - 2)>();  // tile 0 (nkt >= 2 >= kAttBufs - 1)
+    if (kAttBufs - 1 < nkt) {
+      stage_k_tile(Kh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][0], wave, lane);
+      stage_v_tile(Vh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][1], wave, lane);
+    }
+    if (active) attn_tile<true, false, SAFE>(lds[0][0], lds[0][1], qb, 0, L, j, hh, negc, lsum, o);
+    for (int kt = 1; kt < nkt - 1; ++kt) {
+      if (kt + kAttBufs - 2 < nkt)  // K and V: 4 loads per younger tile in flight
+        tile_barrier<4 * (kAttBufs - 2)>();
+      else
+        tile_barrier<0>();
+      if (kt + kAttBufs - 1 < nkt) {
+        const int b = (kt + kAttBufs - 1) % kAttBufs;
+        stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[b][0], wave, lane);
+        stage_v_tile(Vh, kt + kAttBufs - 1, Lpad, lds[b][1], wave, lane);
+      }
+      if (active)
+        attn_tile<false, false, SAFE>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negc, lsum, o);
+    }
+    tile_barrier<0>();
+    if (active)
+      attn_tile<false, true, SAFE>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L,
+                                   j, hh, negc, lsum, o);
+  };
+  sweep(std::integral_constant<bool, false>{});
+  // Overflow check of the fixed-shift sweep (a key far above the first ones): the guarded sweep again,
+  // by the whole workgroup (it streams K/V through the shared LDS ring), if any of its rows failed.
+  bool bad = false;
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt) {
-    lsum[qt] = 0.f;
-    negc[qt] = o[qt][0] = o[qt][1] = zero16();
-  }
+    bad |= !(lsum[qt] + __shfl_xor(lsum[qt], 32) <= kAttSafeSum);
+    float om = 0.f;
 #pragma unroll
-  for (int i = 0; i < kAttBufs - 1; ++i)
-    if (i < nkt) {
-      stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
-      stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
-    }
-  tile_barrier<4 * (kAttBufs - 2)>();  // tile 0 (nkt >= 2 >= kAttBufs - 1)
-  if (kAttBufs - 1 < nkt) {
-    stage_k_tile(Kh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][0], wave, lane);
-    stage_v_tile(Vh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][1], wave, lane);
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) om = fmaxf(om, fabsf(o[qt][dt][r]));
+    bad |= !(om <= 3.0e38f);
   }
-  if (active) attn_tile<true, false>(lds[0][0], lds[0][1], qb, 0, L, j, hh, negc, lsum, o);
-  for (int kt = 1; kt < nkt - 1; ++kt) {
-    if (kt + kAttBufs - 2 < nkt)  // K and V: 4 loads per younger tile in flight
-      tile_barrier<4 * (kAttBufs - 2)>();
-    else
-      tile_barrier<0>();
-    if (kt + kAttBufs - 1 < nkt) {
-      const int b = (kt + kAttBufs - 1) % kAttBufs;
-      stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[b][0], wave, lane);
-      stage_v_tile(Vh, kt + kAttBufs - 1, Lpad, lds[b][1], wave, lane);
-    }
-    if (active) attn_tile<false, false>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negc, lsum, o);
-  }
-  tile_barrier<0>();
+  if (__syncthreads_or(active && bad)) sweep(std::integral_constant<bool, true>{});
   if (!active) return;
-  attn_tile<false, true>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L, j, hh,
-                         negc, lsum, o);
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt)
     attn_store(o[qt], q0 + 32 * qt + j, L, s, h, hh, mode, T, F, G, lsum[qt] + __shfl_xor(lsum[qt], 32), O);
