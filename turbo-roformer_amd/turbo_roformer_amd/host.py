@@ -67,14 +67,25 @@ class HostPath:
 
     # -------------------------------------------------------------------------------------- forward parts
     @torch.no_grad()
+    def stft(self, raw: Tensor) -> Tensor:
+        """(b, 2, n) -> complex STFT (b*2, bins, frames) of the mixture."""
+        b, s, n = raw.shape
+        return torch.stft(raw.reshape(b * s, n).float().to(self.device), **self.stft_kw, window=self.window,
+                          return_complex=True)
+
+    @staticmethod
+    def features(st: Tensor, b: int) -> Tensor:
+        """Complex STFT (b*2, bins, frames) -> real features (b, frames, bins*2*2), ordered (bin, channel,
+        re/im) per frame."""
+        r = torch.view_as_real(st)  # (b*s, bins, T, 2)
+        bs, nb, T = r.shape[0], r.shape[1], r.shape[2]
+        s = bs // b
+        return r.view(b, s, nb, T, 2).permute(0, 3, 2, 1, 4).reshape(b, T, nb * s * 2)
+
+    @torch.no_grad()
     def spectrogram(self, raw: Tensor) -> Tensor:
         """(b, 2, n) -> real STFT (b, frames, bins*2*2) with per-frame features ordered (bin, channel, re/im)."""
-        b, s, n = raw.shape
-        st = torch.stft(raw.reshape(b * s, n).float().to(self.device), **self.stft_kw, window=self.window,
-                        return_complex=True)
-        st = torch.view_as_real(st)  # (b*s, bins, T, 2)
-        nb, T = st.shape[1], st.shape[2]
-        return st.view(b, s, nb, T, 2).permute(0, 3, 2, 1, 4).reshape(b, T, nb * s * 2)
+        return self.features(self.stft(raw), raw.shape[0])
 
     @torch.no_grad()
     def band_split(self, feats: Tensor) -> Tensor:
@@ -102,11 +113,12 @@ class HostPath:
         return mask.view(b, T, self.mask_width)
 
     @torch.no_grad()
-    def apply(self, raw: Tensor, mask: Tensor) -> Tensor:
-        """Complex-multiply the mask into the mixture STFT and invert: (b, 2, hop*(frames-1))."""
+    def apply(self, raw: Tensor, mask: Tensor, st: Tensor | None = None) -> Tensor:
+        """Complex-multiply the mask into the mixture STFT and invert: (b, 2, hop*(frames-1)).  ``st``: the
+        mixture's complex STFT if already computed (``stft(raw)``)."""
         b, s, n = raw.shape
-        st = torch.stft(raw.reshape(b * s, n).float().to(self.device), **self.stft_kw, window=self.window,
-                        return_complex=True)  # (b*s, bins, T)
+        if st is None:
+            st = self.stft(raw)  # (b*s, bins, T)
         nb, T = st.shape[1], st.shape[2]
         m = torch.view_as_complex(mask.reshape(b, T, nb, s, 2).permute(0, 3, 2, 1, 4).contiguous())  # (b, s, bins, T)
         out = torch.istft(st * m.reshape(b * s, nb, T), **self.stft_kw, window=self.window, return_complex=False)

@@ -90,13 +90,14 @@ class Separator:
     def forward_chunks(self, chunks: torch.Tensor) -> torch.Tensor:
         """(b, 2, C) chunks -> (b, 2, hop * (frames - 1)) instrumental predictions, b chunks batched."""
         raw = chunks.to(self.device, torch.float32)
-        feats = self.host.spectrogram(raw)  # (b, T, bins * 2 * 2)
+        st = self.host.stft(raw)  # (b * 2, bins, T) complex, reused for the mask multiply
+        feats = self.host.features(st, raw.shape[0])  # (b, T, bins * 2 * 2)
         b, T = feats.shape[:2]
         F = len(self.band_split.dims)
         Xd = self.band_split(feats.contiguous())  # (b * T * F, 256)
         self.stack(Xd, b, T, F)
         mask = self.mask_head(Xd, b * T).view(b, T, -1)
-        return self.host.apply(raw, mask)
+        return self.host.apply(raw, mask, st)
 
     @torch.inference_mode()
     def separate(self, mix, sr: int = SR, overlap: float = 2.0,
