@@ -6,9 +6,10 @@ band-split into 62 bands of 256-d tokens, through the 24 sub-layers of the 12-bl
 tokens, resident in HBM (a device copy restores the input before each step, inside the timed region).
 
 Prints one JSON line: stack forwards/s, the time-attention kernel's TFLOP/s against the bf16 dense MFMA
-peak (measured with HIP events on the launch stream over the timed region), and a CPU baseline: the
-fp32 restructured torch path (the oracle) timed on the host's cores for one stack forward of the same
-chunk, whose output also gives the mask SNR of the GPU path.
+peak (measured with HIP events on the launch stream over the timed region), and a CPU baseline timed on
+the host's cores for one stack forward of the same chunk: the oracle's AVX512-BF16 CPU stack (bf16
+operands, fp32 accumulators, the arithmetic of the reference's CPU kernels), with the fp32 restructured
+torch path beside it, whose output also gives the mask SNR of the GPU path.
 
 The mask head after the stack (final norm + 62 band MLPs + GLU, one HIP kernel) is timed on the chunk's
 stack output beside it, with its own CPU time (the oracle's fp32 mask estimator) and accuracy.
@@ -17,8 +18,8 @@ The band split before the stack (62 band RMSNorms + Linears, one HIP kernel) pro
 the GPU and is timed the same way.
 
 It also separates a synthetic 4:12 song end to end (for the 29 chunks: one band-split launch, one batched
-stack forward and one mask-head launch on the GPU, STFT / iSTFT in PyTorch on the GPU, overlap-add on the
-CPU) and reports its real-time factor.
+stack forward and one mask-head launch on the GPU, STFT / iSTFT in PyTorch on the GPU, the Hamming
+overlap-add as a HIP kernel) and reports its real-time factor.
 
     python bench.py [--steps K] [--warmup W] [--precision ff_fp16|ff_split|bf16] [--no-cpu] [--no-song]
 """
@@ -77,17 +78,6 @@ def tune_malloc() -> None:
         libc.mallopt(-1, 2_000_000_000)  # M_TRIM_THRESHOLD
     except (OSError, AttributeError):
         pass
-
-
-def cpu_flags() -> set[str]:
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("flags"):
-                    return set(line.split(":", 1)[1].split())
-    except OSError:
-        pass
-    return set()
 
 
 def main() -> int:
@@ -272,7 +262,7 @@ def main() -> int:
         del sep
 
     if not a.no_cpu:
-        from oracle import folded, reference
+        from oracle import cpu_stack, folded, reference
 
         tune_malloc()
         threads = torch.get_num_threads()
@@ -294,16 +284,48 @@ def main() -> int:
         result["mask_head"]["cpu_sample"] = f"oracle fp32 mask estimator on {threads} threads, one chunk"
         # the head alone: HIP mask head on the fp32 stack output against the fp32 mask estimator
         result["mask_head"]["head_snr_db_vs_fp32"] = round(signals.snr_db(m_ref.numpy(), mask_of(ref).numpy()), 2)
-        result["cpu_baseline"] = {
-            "value": round(1.0 / cpu_s, 5),
-            "unit": "stack forwards/s",
-            "cores": threads,
-            "kind": "port",
-            "sample": f"one fp32 stack forward (24 sub-layers, {T}x{F} tokens) of the restructured torch path "
-                      f"(fast.py _transformer_torch restated), {cpu_s:.1f} s, avx512_bf16="
-                      f"{'avx512_bf16' in cpu_flags()}",
-            "gpu_speedup": round((1e3 / ms) * cpu_s, 1),
-        }
+        torch_fp32 = {"s_per_forward": round(cpu_s, 2), "gpu_speedup": round((1e3 / ms) * cpu_s, 1)}
+        if cpu_stack.supported():
+            # the kernel-class CPU baseline: the AVX512-BF16 stack (bf16 operands, fp32 accumulators), one
+            # warm-up forward (it grows and first-touches its work buffers), then the best of two
+            cs = cpu_stack.CpuStack(layers, threads)
+            print(f"bench: cpu baseline, AVX512-BF16 stack forwards on {threads} threads", file=sys.stderr,
+                  flush=True)
+            cs(X0)
+            ph0 = cs.phase_seconds()
+            runs = []
+            for _ in range(2):
+                t6 = time.perf_counter()
+                y_cpu = cs(X0)
+                runs.append(time.perf_counter() - t6)
+            ph1 = cs.phase_seconds()
+            cpu_k_s = min(runs)
+            m_cpu = reference.mask_from_stack(y_cpu, sd, cfg)
+            result["cpu_baseline"] = {
+                "value": round(1.0 / cpu_k_s, 5),
+                "unit": "stack forwards/s",
+                "cores": threads,
+                "kind": "port",
+                "sample": f"one stack forward (24 sub-layers, {T}x{F} tokens) of the AVX512-BF16 CPU stack "
+                          f"(oracle/cpu_stack.cpp: vdpbf16ps GEMMs and attention with fused epilogues, bf16 "
+                          f"operands, fp32 accumulators and residual), best of {len(runs)} after a warm-up, "
+                          f"{cpu_k_s:.2f} s",
+                "gpu_speedup": round((1e3 / ms) * cpu_k_s, 1),
+                "mask_snr_db_vs_fp32": round(signals.snr_db(m_ref.numpy(), m_cpu.numpy()), 2),
+                "phase_s": {k: round((ph1[k] - ph0[k]) / len(runs), 3) for k in cpu_stack.PHASES},
+                "torch_fp32": torch_fp32,
+            }
+        else:
+            result["cpu_baseline"] = {
+                "value": round(1.0 / cpu_s, 5),
+                "unit": "stack forwards/s",
+                "cores": threads,
+                "kind": "port",
+                "sample": f"one fp32 stack forward (24 sub-layers, {T}x{F} tokens) of the restructured torch "
+                          f"path (fast.py _transformer_torch restated), {cpu_s:.1f} s; this CPU has no "
+                          f"AVX512-BF16 for the kernel-class CPU stack",
+                "gpu_speedup": torch_fp32["gpu_speedup"],
+            }
         result["parity"] = {"mask_snr_db_vs_fp32": round(snr_mask, 2), "stack_out_snr_db_vs_fp32": round(snr_x, 2)}
         for p, v in snr_alts.items():
             result["parity"][f"mask_snr_db_vs_fp32_{p}"] = round(v, 2)
