@@ -834,7 +834,8 @@ void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int
 constexpr int kMlpWaves = 8;
 constexpr int kOutStages = 8;                // 32 k-steps of W_out, 4 per stage
 constexpr int kFfStages = kHidden / 32;      // one 32-wide hidden tile per stage
-constexpr int kMlpPrefetch = 4;              // LDS operands read ahead of their MFMA
+constexpr int kMlpPrefetch = 4;              // LDS operands read ahead of their MFMA (out-projection)
+constexpr int kMlpFfPrefetch = 2;            // the same in the feed-forward stages (registers are short)
 
 // erf-GELU x Phi(x) = max(x, 0) - 0.5|x| erfc(|x|/sqrt 2), with erfc from Abramowitz & Stegun 7.1.26
 // (|error of erf| <= 1.5e-7): erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-z^2),
@@ -900,8 +901,8 @@ __device__ __forceinline__ f32x16 mfma_ff(u32x4 a, u32x4 b, f32x16 c) {
 
 // This wave's 4 of stage s's 32 operand blocks into LDS.  Stages 0..7: W_out k-steps 4s..4s+3 of the
 // 8 tiles.  Feed-forward stage u = s - 8 (0..32): blocks 0..15 are W1 tile u (k-steps 0..15; none for
-// u = 32), blocks 16..31 W2 k-steps 2(u-1), 2(u-1)+1 of the 8 output tiles (for u = 0 k-steps 0, 1:
-// finite values that meet zero B operands).  Nothing for s past the last stage.
+// u = 32), blocks 16..31 W2 k-steps 2(u-1), 2(u-1)+1 of the 8 output tiles (for u = 0 k-steps 0, 1,
+// loaded but not read).  Nothing for s past the last stage.
 __device__ __forceinline__ void mlp_issue(int s, u32x4* dst, const u32x4* wo, const u32x4* w1, const u32x4* w2,
                                           int wave, int lane) {
 #pragma unroll
@@ -924,39 +925,29 @@ __device__ __forceinline__ void mlp_issue(int s, u32x4* dst, const u32x4* wo, co
   }
 }
 
-// Operand block of MFMA i of a feed-forward stage.  MODE 0: FF1(u) and FF2(u-1) alternate (even i: FF1
-// k-step i/2, block i/2; odd i: FF2 step j = i/2 into output tile j%8 with hidden half j/8, block
-// 16 + 2(j%8) + j/8), so the FF1 accumulator chain has an independent MFMA between its links.
-// MODE 2: FF2 only (step j = i).
-template <int MODE>
-__device__ __forceinline__ constexpr int ff_block_of(int i) {
-  const int j = MODE == 2 ? i : i >> 1;
-  if (MODE == 0 && !(i & 1)) return i >> 1;
-  return 16 + 2 * (j % 8) + j / 8;
+// One feed-forward stage u, the same in every wave.  Stage u's LDS buffer holds W1 of hidden tile u
+// (blocks 0..15, k-steps 0..15) and W2 of tile u-1 (block 16 + 2t + c: output tile t, hidden half c).
+//   MFMAs 0..15:   FF1(u)   h := b1(u) + xn . W1(u)^T, one accumulator chain;
+//   MFMAs 16..31:  FF2(u-1) acc[t] += gelu(h(u-1))[half c] . W2(u-1, t, c)^T, step j = 16 + 8c + t.
+// GELU of the previous stage's h is spread between these MFMAs, value v after MFMA 3v/2, so that
+// neither wave of a SIMD runs a long VALU-only stretch: on gfx950 VALU work of one wave overlaps the
+// MFMAs of the other wave on its SIMD (measured: 65-80% of it hidden), while VALU work between a wave's
+// own MFMAs is barely hidden at all.  Values 0..7 (the B operand of steps 16..23) are done by MFMA 10,
+// values 8..15 by MFMA 22.
+// KIND 0: the first stage (FF1(0) only); KIND 1: stages 1..31; KIND 2: the last stage (FF2(31) only).
+constexpr int mlp_gelu_slot(int v) { return (3 * v) / 2; }
+
+__device__ __forceinline__ constexpr int mlp_block_of(int m) {
+  return m < 16 ? m : 16 + 2 * ((m - 16) % 8) + (m - 16) / 8;
 }
 
-// gelu(h) as the two register-order B operands of FF2.
-template <bool F16>
-__device__ __forceinline__ void mlp_gelu(const f32x16& h, u32x4 (&hb)[2]) {
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    float v[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) v[r] = gelu_erf(h[8 * c + r]);
-    hb[c] = u32x4{pk_ff<F16>(v[0], v[1]), pk_ff<F16>(v[2], v[3]), pk_ff<F16>(v[4], v[5]), pk_ff<F16>(v[6], v[7])};
-  }
-}
-
-// The MFMAs of one feed-forward stage, each A operand read from LDS kMlpPrefetch MFMAs ahead (the
-// sched barriers keep that order).  MODE 0: h := b1(u) + xn . W1(u)^T and acc += hb . W2(u-1)^T,
-// interleaved; MODE 2: only the latter.
-template <bool F16, int MODE>
-__device__ __forceinline__ void mlp_ff_block(const u32x4* Ls, const f32x4* b1s, const u32x4 (&xb)[16],
-                                             const u32x4 (&hb)[2], int u, int hh, int lane, f32x16& h,
-                                             f32x16 (&acc)[8]) {
-  constexpr int N = MODE == 0 ? 32 : 16;
-  constexpr int D = kMlpPrefetch;
-  if (MODE == 0) {
+template <bool F16, int KIND>
+__device__ __forceinline__ void mlp_ff_pstage(const u32x4* Ls, const f32x4* b1s, const u32x4 (&xb)[16], int u,
+                                              int hh, int lane, f32x16& h, f32x16 (&acc)[8]) {
+  constexpr int D = kMlpFfPrefetch;
+  constexpr int m0 = KIND == 2 ? 16 : 0, m1 = KIND == 0 ? 16 : 32;
+  const f32x16 hp = h;  // h(u-1), the GELU input (KIND 1, 2)
+  if (KIND != 2) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 b = b1s[8 * u + 2 * g + hh];  // h starts at b1
@@ -964,18 +955,37 @@ __device__ __forceinline__ void mlp_ff_block(const u32x4* Ls, const f32x4* b1s, 
       for (int r = 0; r < 4; ++r) h[4 * g + r] = b[r];
     }
   }
+  u32x4 hb[2] = {zero4(), zero4()};
+  float gv[2];
+  auto gelu_value = [&](int v) {
+    gv[v & 1] = gelu_erf(hp[v]);
+    if (v & 1) hb[v >> 3][(v & 7) >> 1] = pk_ff<F16>(gv[0], gv[1]);
+  };
+  if (KIND == 2) {  // nothing to hide the first half behind
+#pragma unroll
+    for (int v = 0; v < 8; ++v) gelu_value(v);
+  }
   u32x4 a[D];
 #pragma unroll
-  for (int i = 0; i < D; ++i) a[i] = Ls[ff_block_of<MODE>(i) * 64 + lane];
+  for (int i = 0; i < D; ++i)
+    if (m0 + i < m1) a[i] = Ls[mlp_block_of(m0 + i) * 64 + lane];
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    if (MODE == 0 && !(i & 1)) {
-      h = mfma_ff<F16>(a[i % D], xb[i >> 1], h);
+  for (int m = m0; m < m1; ++m) {
+    const int i = m - m0;
+    if (m < 16) {
+      h = mfma_ff<F16>(a[i % D], xb[m], h);
     } else {
-      const int j = MODE == 2 ? i : i >> 1;
+      const int j = m - 16;
       acc[j % 8] = mfma_ff<F16>(a[i % D], hb[j / 8], acc[j % 8]);
     }
-    if (i + D < N) a[i % D] = Ls[ff_block_of<MODE>(i + D) * 64 + lane];
+    if (m + D < m1) a[i % D] = Ls[mlp_block_of(m + D) * 64 + lane];
+    if (KIND == 1) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (mlp_gelu_slot(v) == m) gelu_value(v);
+    } else if (KIND == 2) {
+      if (m < 24) gelu_value(8 + (m - 16));  // values 8..15 beside steps 16..23 (half 0)
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -995,54 +1005,35 @@ __device__ __forceinline__ void mlp_out_block(const u32x4* Ls, const u32x4 (&cur
   }
 }
 
-// Feed-forward stage u read from LDS buffer Lcur, the other buffer being Lnext (both compile-time
-// buffers, see mlp_ff_stages).
-template <bool F16>
-__device__ __forceinline__ void mlp_ff_stage(int u, u32x4* Lcur, u32x4* Lnext, f32x16 (&acc)[8],
-                                             const u32x4 (&xb)[16], const f32x4* b1s, const u32x4* wo,
-                                             const u32x4* w1, const u32x4* w2, int wave, int lane, int hh,
-                                             bool early, f32x16& h, u32x4 (&hb)[2]) {
-  const int s = kOutStages + u;
-  if (!early && u > 0) {
-    stage_barrier();
-    mlp_issue(s + 1, Lnext, wo, w1, w2, wave, lane);
-  }
-  mlp_ff_block<F16, 0>(Lcur, b1s, xb, hb, u, hh, lane, h, acc);
-  if (early) {
-    stage_barrier();
-    mlp_issue(s + 2, Lcur, wo, w1, w2, wave, lane);  // nothing past the last stage
-  }
-  mlp_gelu<F16>(h, hb);
-}
-
-// The 33 feed-forward stages.  Stage u holds W1 of hidden tile u and W2 of tile u-1, and every wave runs
-// FF2(u-1) interleaved with FF1(u), then GELU(u) (stage 0 multiplies its W2 blocks by hb = 0; stage 32 is
-// FF2(31) alone).  The waves differ only in where the stage barrier falls: before the MFMAs ("late"
-// waves) or between the MFMAs and GELU ("early" waves, plus one barrier up front, so both take 33).
-// Waves w and w + 4 of a workgroup share a SIMD (read from HW_ID on gfx950), so pairing early waves
-// 4..7 with late waves 0..3 puts the two waves of a SIMD in opposite phases, one's GELU beside the
-// other's MFMAs.  Stage u+2 is loaded into stage u's buffer only after barrier u+1, when both kinds of
-// wave are done with it.  Stages go in pairs so that each one's buffers are compile-time constants: the
-// compiler can then tell the operand reads from the direct-to-LDS loads into the other buffer, and does
-// not wait for those loads before reading.
+// The 33 feed-forward stages.  Every wave runs the same sequence; before stage u all waves meet (stage
+// u's operands have landed and stage u-1's buffer is free) and stage u+1's operands are issued into
+// that buffer.  Stages go in pairs so that each one's buffers are compile-time constants: the compiler
+// can then tell the operand reads from the direct-to-LDS loads into the other buffer, and does not wait
+// for those loads before reading.
 template <bool F16>
 __device__ __forceinline__ void mlp_ff_stages(f32x16 (&acc)[8], const u32x4 (&xb)[16], u32x4 (*lds)[32 * 64],
                                               const f32x4* b1s, const u32x4* wo, const u32x4* w1,
                                               const u32x4* w2, int wave, int lane, int hh) {
   constexpr int s0 = kOutStages;
-  static_assert(s0 % 2 == 0 && kFfStages % 2 == 0, "stage pairs start on buffer 0");
-  const bool early = wave >= kMlpWaves / 2;
-  u32x4 hb[2] = {zero4(), zero4()};
+  static_assert(s0 % 2 == 0 && kFfStages == 32, "stage 0 in buffer 0, stages 1..30 in pairs");
   f32x16 h = zero16();
   stage_barrier();
   mlp_issue(s0 + 1, lds[1], wo, w1, w2, wave, lane);
+  mlp_ff_pstage<F16, 0>(lds[0], b1s, xb, 0, hh, lane, h, acc);
 #pragma clang loop unroll(disable)
-  for (int u = 0; u < kFfStages; u += 2) {
-    mlp_ff_stage<F16>(u, lds[0], lds[1], acc, xb, b1s, wo, w1, w2, wave, lane, hh, early, h, hb);
-    mlp_ff_stage<F16>(u + 1, lds[1], lds[0], acc, xb, b1s, wo, w1, w2, wave, lane, hh, early, h, hb);
+  for (int u = 1; u < kFfStages - 1; u += 2) {
+    stage_barrier();
+    mlp_issue(s0 + u + 1, lds[0], wo, w1, w2, wave, lane);
+    mlp_ff_pstage<F16, 1>(lds[1], b1s, xb, u, hh, lane, h, acc);
+    stage_barrier();
+    mlp_issue(s0 + u + 2, lds[1], wo, w1, w2, wave, lane);
+    mlp_ff_pstage<F16, 1>(lds[0], b1s, xb, u + 1, hh, lane, h, acc);
   }
-  if (!early) stage_barrier();
-  mlp_ff_block<F16, 2>(lds[0], b1s, xb, hb, kFfStages, hh, lane, h, acc);
+  stage_barrier();
+  mlp_issue(s0 + kFfStages, lds[0], wo, w1, w2, wave, lane);
+  mlp_ff_pstage<F16, 1>(lds[1], b1s, xb, kFfStages - 1, hh, lane, h, acc);
+  stage_barrier();
+  mlp_ff_pstage<F16, 2>(lds[0], b1s, xb, kFfStages, hh, lane, h, acc);
 }
 
 template <bool OUTPROJ, bool FF, bool F16>
