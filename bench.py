@@ -287,14 +287,14 @@ def main() -> int:
         torch_fp32 = {"s_per_forward": round(cpu_s, 2), "gpu_speedup": round((1e3 / ms) * cpu_s, 1)}
         if cpu_stack.supported():
             # the kernel-class CPU baseline: the AVX512-BF16 stack (bf16 operands, fp32 accumulators), one
-            # warm-up forward (it grows and first-touches its work buffers), then the best of two
+            # warm-up forward (it grows and first-touches its work buffers), then the best of three
             cs = cpu_stack.CpuStack(layers, threads)
             print(f"bench: cpu baseline, AVX512-BF16 stack forwards on {threads} threads", file=sys.stderr,
                   flush=True)
             cs(X0)
             ph0 = cs.phase_seconds()
             runs = []
-            for _ in range(2):
+            for _ in range(3):
                 t6 = time.perf_counter()
                 y_cpu = cs(X0)
                 runs.append(time.perf_counter() - t6)
