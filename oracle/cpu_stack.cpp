@@ -18,8 +18,8 @@
 //       same rows as the bf16 input of the next GEMM;
 //     - FF1: bias + exact-erf GELU, bf16 out.
 // * Attention per (sequence, head), 6 query rows at a time, exact softmax: pass 1 the scores of all keys
-//   (64-key tiles) and the row max, pass 2 2^((s - max) log2 e) rounded to bf16 and summed
-//   in fp32, pass 3 P V with the same 6 x 64 tile; the 1/sum, the head's sigmoid gate and the head
+//   (64-key tiles) and the row max, pass 2 e = 2^((s - max) log2 e), summed in fp32 and stored rounded to
+//   bf16, pass 3 P V with the same 6 x 64 tile; the 1/sum, the head's sigmoid gate and the head
 //   merge are applied when the tile is written.
 // * Work is spread over std::threads by an atomic task counter (row blocks of 48 tokens for the GEMMs,
 //   (sequence, head) pairs for the attention).  A token's result does not depend on the thread count or
@@ -64,8 +64,6 @@ inline int32_t ld32(const bf16* p) {
   std::memcpy(&v, p, 4);
   return v;
 }
-
-inline __m512 bf16x16_to_ps(__m256i h) { return _mm512_castsi512_ps(_mm512_slli_epi32(_mm512_cvtepu16_epi32(h), 16)); }
 
 inline __m256i ps_to_bf16x16(__m512 x) { return (__m256i)_mm512_cvtneps_pbh(x); }
 
@@ -399,9 +397,8 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
               const __mmask16 valid = c + 16 <= L ? __mmask16(0xffff) : __mmask16((1u << (L - c)) - 1);
               __m512 p = exp2_ps(_mm512_fmsub_ps(_mm512_loadu_ps(&S[r * lp + c]), _mm512_set1_ps(kLog2e), mb));
               p = _mm512_maskz_mov_ps(valid, p);
-              const __m256i pb = ps_to_bf16x16(p);
-              _mm256_storeu_si256((__m256i*)&Pb[r * lp + c], pb);
-              sum = _mm512_add_ps(sum, bf16x16_to_ps(pb));
+              _mm256_storeu_si256((__m256i*)&Pb[r * lp + c], ps_to_bf16x16(p));
+              sum = _mm512_add_ps(sum, p);  // the fp32 values, before their bf16 rounding
             }
             inv[r] = 1.f / hsum(sum);
           }
