@@ -1,9 +1,11 @@
 /*
  * trf_hip.h - C ABI of the MI355X (gfx950) BS-RoFormer transformer stack.
  *
- * The library replaces the seven AVX512-BF16 torch ops of LoggeL/turbo-roformer
- * (src/turbo_roformer/csrc/kernels.cpp:644-652) and the stack loop that calls them
- * (FastBSRoformer._transformer_cpp, src/turbo_roformer/fast.py:269-341) with HIP
+ * The library replaces the AVX512-BF16 torch ops of LoggeL/turbo-roformer on the default path
+ * (src/turbo_roformer/csrc/kernels.cpp:644-652: add_rmsnorm, qkv_rope_gemm, attention,
+ * gemm_res_norm, gemm_gelu; the other two, rope_pack and gate_merge, serve the unfused and SDPA
+ * variants, and their work is done inside trf_qkv_rope_gemm and trf_attention) and the stack loop that
+ * calls them (FastBSRoformer._transformer_cpp, src/turbo_roformer/fast.py:269-341) with HIP
  * kernels, and the steps either side of it: the band split that feeds the stack and the mask head
  * that follows it (fast.py:377-387), plus the overlap-add that assembles a song from its chunks.
  * Every entry point takes plain device pointers, sizes and a HIP stream;
