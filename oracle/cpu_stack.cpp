@@ -219,11 +219,6 @@ struct Stack {
   Buffer<bf16> xn, ao, h, q, k, v;
   Buffer<float> gates, rc, rs;
 
-  template <class Buf>
-  static void grow(Buf& buf, size_t n) {
-    buf.grow(n);
-  }
-
   // xn[n] = bf16(X[n] / max(|X[n]|, 1e-12)) for rows [r0, r1)
   static void norm_rows(const float* X, bf16* xn, int64_t r0, int64_t r1) {
     for (int64_t n = r0; n < r1; ++n) {
@@ -266,15 +261,15 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
   const int64_t Lmax = std::max(T, F);
   const int64_t seq_stride = round_up(Lmax, 64) * kDh;  // elements of one (sequence, head) in q, k, v
   const int64_t max_seqs = std::max<int64_t>(int64_t(b) * F, int64_t(b) * T);
-  grow(xn, size_t(N) * kDim);
-  grow(ao, size_t(N) * kH * kDh);
-  grow(h, size_t(N) * kFf);
-  grow(gates, size_t(N) * kGates);
-  grow(q, size_t(max_seqs) * kH * seq_stride);
-  grow(k, size_t(max_seqs) * kH * seq_stride);
-  grow(v, size_t(max_seqs) * kH * seq_stride);
-  grow(rc, size_t(Lmax) * kDh);
-  grow(rs, size_t(Lmax) * kDh);
+  xn.grow(size_t(N) * kDim);
+  ao.grow(size_t(N) * kH * kDh);
+  h.grow(size_t(N) * kFf);
+  gates.grow(size_t(N) * kGates);
+  q.grow(size_t(max_seqs) * kH * seq_stride);
+  k.grow(size_t(max_seqs) * kH * seq_stride);
+  v.grow(size_t(max_seqs) * kH * seq_stride);
+  rc.grow(size_t(Lmax) * kDh);
+  rs.grow(size_t(Lmax) * kDh);
 
   timed(kPhNorm, [&] {
     parallel_for(ntask, threads, [&](int t) {
