@@ -68,6 +68,31 @@ def measured_traffic() -> float | None:
     return None
 
 
+def host_cpu() -> dict:
+    """The host CPU the baseline runs on: model name, logical CPUs this process may use, physical cores
+    (distinct (package, core) pairs in /proc/cpuinfo) and whether it has AVX512-BF16."""
+    info = {"model": "unknown", "cpus_usable": len(os.sched_getaffinity(0))}
+    try:
+        text = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return info
+    cores, pkg, flags = set(), "0", ""
+    for line in text.splitlines():
+        key, _, val = line.partition(":")
+        key, val = key.strip(), val.strip()
+        if key == "model name" and info["model"] == "unknown":
+            info["model"] = val
+        elif key == "physical id":
+            pkg = val
+        elif key == "core id":
+            cores.add((pkg, val))
+        elif key == "flags" and not flags:
+            flags = val
+    info["physical_cores"] = len(cores) or None
+    info["avx512_bf16"] = "avx512_bf16" in flags.split()
+    return info
+
+
 def tune_malloc() -> None:
     """glibc: keep large blocks on the heap (the reference's tune_malloc, separator.py:32-54)."""
     try:
@@ -216,7 +241,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "bf16+fp16",
+        "dtype_detail": ("bf16 MFMA operands for the QKV GEMM, both attentions and the out-projection; fp16 "
+                         "operands for the two feed-forward GEMMs (ff_fp16); fp32 accumulation, residual stream, "
+                         "norms, rotary and softmax statistics") if a.precision == "ff_fp16" else a.precision,
         "data": "synthetic (seeded Gaussian + pink-noise stereo mix, peak 0.5; seeded random weights)",
         "config": {
             "workload": "BS-RoFormer 12-block transformer stack (24 sub-layers) on one 17 s chunk",
@@ -248,7 +276,7 @@ def main() -> int:
         # the mask head on the kernels, STFT and iSTFT in PyTorch on the same GPU, Hamming overlap-add on the CPU
         from turbo_roformer_amd.separator import Separator
 
-        sep = Separator(sd, cfg, T, "cuda", precision=a.precision)
+        sep = Separator(sd, cfg, T, "cuda", stack_precision=a.precision, batch_chunks=0)
         song = signals.song(SONG_SECONDS, seed=a.seed)
         sep.separate(song[:, : sep.chunk])  # warm-up: tables, workspace
         torch.cuda.synchronize()
@@ -259,6 +287,20 @@ def main() -> int:
         print(f"bench: {SONG_SECONDS:.0f} s song separated in {wall:.3f} s", file=sys.stderr, flush=True)
         result["song"] = {"audio_s": SONG_SECONDS, "chunks": sep.n_chunks(song.shape[1]), "wall_s": round(wall, 3),
                           "rtf": round(wall / SONG_SECONDS, 5), "overlap": 2.0}
+        if not a.no_cpu:
+            # quality on the song's first chunk (the reference's --quality-seconds, bench_synthetic.py:78-84):
+            # the same separation by the fp32 oracle forward, same chunk schedule and overlap-add
+            from oracle import reference
+            from turbo_roformer_amd.chunking import overlap_add
+
+            head_n = sep.chunk
+            print(f"bench: song quality, fp32 oracle on the first {head_n / 44100:.1f} s", file=sys.stderr,
+                  flush=True)
+            fast = sep.separate(song[:, :head_n])
+            exact = overlap_add(torch.from_numpy(np.ascontiguousarray(song[:, :head_n])), sep.chunk, 2.0,
+                                lambda c: reference.forward(c, sd, cfg), batch=1).numpy()
+            result["song"]["quality_seconds"] = round(head_n / 44100, 2)
+            result["song"]["snr_vs_fp32_db"] = round(signals.snr_db(exact, fast), 2)
         del sep
 
     if not a.no_cpu:
@@ -266,6 +308,7 @@ def main() -> int:
 
         tune_malloc()
         threads = torch.get_num_threads()
+        cpu_info = host_cpu()
         layers = folded.fold(sd, cfg["depth"])
         print(f"bench: cpu baseline, one fp32 stack forward on {threads} threads", file=sys.stderr, flush=True)
         t2 = time.perf_counter()
@@ -284,7 +327,22 @@ def main() -> int:
         result["mask_head"]["cpu_sample"] = f"oracle fp32 mask estimator on {threads} threads, one chunk"
         # the head alone: HIP mask head on the fp32 stack output against the fp32 mask estimator
         result["mask_head"]["head_snr_db_vs_fp32"] = round(signals.snr_db(m_ref.numpy(), mask_of(ref).numpy()), 2)
-        torch_fp32 = {"s_per_forward": round(cpu_s, 2), "gpu_speedup": round((1e3 / ms) * cpu_s, 1)}
+        # the reference's published ratio of its fp32 restructured torch stack to its AVX512-BF16 kernel
+        # stack (24.61 s vs 6.07 s per chunk, docs/benchmarks.md:90,104-112)
+        kernel_ratio = 24.61 / 6.07
+        torch_fp32 = {"s_per_forward": round(cpu_s, 2), "gpu_speedup": round((1e3 / ms) * cpu_s, 1),
+                      "reference_kernel_ratio": round(kernel_ratio, 2),
+                      "kernel_equivalent_s": round(cpu_s / kernel_ratio, 2),
+                      "gpu_speedup_vs_kernel_equivalent": round((1e3 / ms) * cpu_s / kernel_ratio, 1)}
+        print(f"bench: cpu baseline, one bf16 (oneDNN GEMMs + SDPA) stack forward on {threads} threads",
+              file=sys.stderr, flush=True)
+        t7 = time.perf_counter()
+        y_b16 = folded.stack_bf16_sdpa(X0, layers)
+        b16_s = time.perf_counter() - t7
+        torch_bf16 = {"s_per_forward": round(b16_s, 2), "gpu_speedup": round((1e3 / ms) * b16_s, 1),
+                      "mask_snr_db_vs_fp32": round(signals.snr_db(
+                          m_ref.numpy(), reference.mask_from_stack(y_b16, sd, cfg).numpy()), 2)}
+        del y_b16
         if cpu_stack.supported():
             # the kernel-class CPU baseline: the AVX512-BF16 stack (bf16 operands, fp32 accumulators), one
             # warm-up forward (it grows and first-touches its work buffers), then the best of three
@@ -313,7 +371,9 @@ def main() -> int:
                 "gpu_speedup": round((1e3 / ms) * cpu_k_s, 1),
                 "mask_snr_db_vs_fp32": round(signals.snr_db(m_ref.numpy(), m_cpu.numpy()), 2),
                 "phase_s": {k: round((ph1[k] - ph0[k]) / len(runs), 3) for k in cpu_stack.PHASES},
+                "host": cpu_info,
                 "torch_fp32": torch_fp32,
+                "torch_bf16": torch_bf16,
             }
         else:
             result["cpu_baseline"] = {
@@ -325,6 +385,9 @@ def main() -> int:
                           f"path (fast.py _transformer_torch restated), {cpu_s:.1f} s; this CPU has no "
                           f"AVX512-BF16 for the kernel-class CPU stack",
                 "gpu_speedup": torch_fp32["gpu_speedup"],
+                "host": cpu_info,
+                "torch_fp32": torch_fp32,
+                "torch_bf16": torch_bf16,
             }
         result["parity"] = {"mask_snr_db_vs_fp32": round(snr_mask, 2), "stack_out_snr_db_vs_fp32": round(snr_x, 2)}
         for p, v in snr_alts.items():

@@ -242,8 +242,10 @@ int trf_band_split(const float* feats, int32_t n_frames, int32_t n_bands, const 
  * for chunks in ascending order, acc[ch][s:s+L] += y[c][ch][:L] * window[:L] and wsum[s:s+L] += window[:L],
  * each term with the reference's two fp32 roundings (product, then sum), so the sums are bitwise those of
  * its loop; a song processed in several batches calls trf_overlap_add once per batch, in chunk order.
- * y [n_chunks][2][y_stride] fp32; starts: device int64 [n_chunks], ascending, each chunk's first sample;
- * window: device fp32 [>= L]; acc [2][n] and wsum [n]: device fp32, zeroed before the first batch. */
+ * y [n_chunks][2][y_stride] fp32; starts: device int64 [n_chunks], ascending, each chunk's first sample
+ * (the library cannot read them on the host: with starts out of order the sums are wrong, but every
+ * access stays in bounds); window: device fp32 [>= L]; acc [2][n] and wsum [n]: device fp32, zeroed
+ * before the first batch. */
 int trf_overlap_add(const float* y, int32_t n_chunks, int64_t y_stride, int32_t L, const int64_t* starts,
                     const float* window, int64_t n, float* acc, float* wsum, trf_stream_t stream);
 

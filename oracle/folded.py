@@ -78,6 +78,41 @@ def ff_sublayer(X: Tensor, P: dict, dtype=torch.float32) -> Tensor:
     return F.linear(h, P["W2"].to(dtype), P["b2"].to(dtype)).float()
 
 
+def attn_sublayer_sdpa(X: Tensor, P: dict, dtype=torch.bfloat16) -> Tensor:
+    """``_attn_torch`` (fast.py:229-249) as the reference runs it in bf16: GEMMs in ``dtype``, rotary in fp32
+    rounded back to ``dtype``, attention by ``F.scaled_dot_product_attention`` in ``dtype`` (scale 1, the
+    1/8 is in W_q)."""
+    b, T, Fq, _ = X.shape
+    xn = l2n(X).to(dtype)
+    qkvg = F.linear(xn, P["W"].to(dtype), P["b"].to(dtype))
+    qkv = qkvg[..., : 3 * H * DH].view(b, T, Fq, 3, H, DH)
+    g = qkvg[..., 3 * H * DH :].float().sigmoid()
+    if P["mode"] == 0:
+        qkv = qkv.permute(3, 0, 2, 4, 1, 5)
+        L = T
+    else:
+        qkv = qkv.permute(3, 0, 1, 4, 2, 5)
+        L = Fq
+    ang = reference.rotary_angles(L, P["freqs"])
+    q, k = reference.rotate(qkv[0], ang), reference.rotate(qkv[1], ang)
+    o = F.scaled_dot_product_attention(q, k, qkv[2], scale=1.0)
+    o = o.permute(0, 3, 1, 2, 4) if P["mode"] == 0 else o.permute(0, 1, 3, 2, 4)
+    o = (o * g.unsqueeze(-1).to(o.dtype)).reshape(b, T, Fq, H * DH)
+    return F.linear(o, P["Wo"].to(dtype)).float()
+
+
+@torch.no_grad()
+def stack_bf16_sdpa(X: Tensor, layers: list[dict]) -> Tensor:
+    """The reference's portable bf16 path (``FastBSRoformer(dtype=bf16, glue="torch", attn="sdpa")``,
+    fast.py:222-266): bf16 GEMMs (oneDNN on the CPU), bf16 SDPA, fp32 residual.  Used as a CPU timing
+    baseline, not as a checker."""
+    X = X.float().clone()
+    for P in layers:
+        X = X + attn_sublayer_sdpa(X, P)
+        X = X + ff_sublayer(X, P, torch.bfloat16)
+    return X
+
+
 @torch.no_grad()
 def stack(X: Tensor, layers: list[dict], dtype=torch.float32) -> Tensor:
     """``_transformer_torch`` (fast.py:259-266) on X (b, T, F, 256) fp32; returns a new tensor."""

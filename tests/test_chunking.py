@@ -3,6 +3,8 @@
 
 from __future__ import annotations
 
+import itertools
+
 import numpy as np
 import pytest
 import torch
@@ -39,14 +41,16 @@ def test_schedule_against_brute_force():
 @pytest.mark.parametrize("n", [1, 100, 999, 1000, 1001, 5000, 12345])
 @pytest.mark.parametrize("overlap", [1.0, 1.5, 2.0, 3.0])
 def test_schedule_covers_signal(n, overlap):
+    """Chunks lie inside the signal, starts strictly increase, and the per-sample chunk count (a
+    difference array summed up) is at least one everywhere."""
     C = min(1000, n)
-    starts = chunk_starts(n, C, step_for(C, overlap))
-    covered = np.zeros(n, bool)
-    for s in starts:
-        assert 0 <= s <= n - C
-        covered[s : s + C] = True
-    assert covered.all()
-    assert starts == sorted(set(starts))
+    starts = np.asarray(chunk_starts(n, C, step_for(C, overlap)))
+    assert (starts >= 0).all() and (starts + C <= n).all()
+    assert (np.diff(starts) > 0).all()
+    delta = np.zeros(n + 1, np.int64)
+    np.add.at(delta, starts, 1)
+    np.add.at(delta, starts + C, -1)
+    assert np.cumsum(delta)[:n].min() >= 1
 
 
 def test_hamming_matches_numpy():
@@ -80,18 +84,37 @@ def test_batches_see_every_chunk_once_in_order():
     assert calls == [(k, n) for k in range(1, n + 1)]
 
 
+def _alternating_gain_model():
+    """A 'model' that scales chunk k by 0.8 (k even) or 1.2 (k odd): neighbouring chunks disagree by 0.4."""
+    k = itertools.count()
+    return lambda c: c * (0.8 if next(k) % 2 == 0 else 1.2)
+
+
 @pytest.mark.parametrize("overlap", [1.5, 2.0, 3.0])
-def test_no_click_with_chunk_dependent_model(overlap):
-    """Chunks that disagree (+-20 % gain) are crossfaded: with a DC input the output is the blend
-    envelope, whose steps stay far below the 0.4 jump of a hard switch."""
+def test_disagreeing_chunks_are_crossfaded(overlap):
+    """On a constant input the windowed sum glides between the two gains; without overlap the output
+    jumps by their whole difference at each seam."""
     n, chunk = 100_000, 16000
-    x = torch.ones(2, n)
-    gains = iter([0.8, 1.2] * 100)
-    y = overlap_add(x, chunk, overlap, lambda c: c * next(gains), batch=1).numpy()
+    ones = torch.ones(2, n)
+    y = overlap_add(ones, chunk, overlap, _alternating_gain_model(), batch=1).numpy()
     assert y.min() >= 0.8 - 1e-6 and y.max() <= 1.2 + 1e-6
-    assert np.abs(np.diff(y, axis=1)).max() < 0.25 * 0.4
-    hard = overlap_add(x, chunk, 1.0, lambda c: c * next(gains), batch=1).numpy()
-    assert np.abs(np.diff(hard, axis=1)).max() > 0.39
+    hard = overlap_add(ones, chunk, 1.0, _alternating_gain_model(), batch=1).numpy()
+    hard_jump = np.abs(np.diff(hard, axis=1)).max()
+    assert hard_jump == pytest.approx(0.4, abs=0.01)
+    assert np.abs(np.diff(y, axis=1)).max() < hard_jump / 4
+
+
+def test_device_overlap_add_checks_starts_on_the_host():
+    """The GPU overlap-add finds a sample's chunks by binary search over the starts: its wrapper rejects
+    starts that are unsorted, repeated or reach outside the song before anything is uploaded."""
+    from turbo_roformer_amd._hip import check_chunk_starts
+
+    assert check_chunk_starts([0, 5, 9], 3, 4, 13) == [0, 5, 9]
+    assert check_chunk_starts(torch.tensor([0, 5]), 2, 4, 9) == [0, 5]
+    for starts, nc, L, n in (([5, 0, 9], 3, 4, 13), ([0, 0], 2, 4, 13), ([0, 5], 3, 4, 13), ([-1, 5], 2, 4, 13),
+                             ([0, 10], 2, 4, 13)):
+        with pytest.raises(ValueError):
+            check_chunk_starts(starts, nc, L, n)
 
 
 def test_as_stereo():

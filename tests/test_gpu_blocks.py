@@ -87,6 +87,9 @@ def test_attention_block_full_shape(stack, sd, x_bf16, mode):
     print(f"  update snr vs fp32 {s_ref:.1f} dB (bf16 design {s_design:.1f} dB), vs emulation {s_emu:.1f} dB")
     assert s_emu >= 45.0
     assert s_ref >= s_design - 1.0
+    # absolute floor against the fp32 forward (the bf16 design measures 47.6-47.8 dB on this input), so a
+    # drift of the emulation cannot move the bar with it
+    assert s_ref >= 46.0
 
 
 def test_feed_forward_block_full_shape(stack, sd, x_bf16):
@@ -118,6 +121,8 @@ def test_feed_forward_block_full_shape(stack, sd, x_bf16):
         assert s_ref >= 90.0
     elif stack.precision == "ff_fp16":
         assert s_ref >= s_design - 1.0 and s_design >= 65.0  # fp16 operands: ~18 dB above bf16
+        assert s_ref >= 66.0  # absolute floor (68.3 dB measured)
     else:
         assert s_ref >= s_design - 1.0
+        assert s_ref >= 48.5  # absolute floor (50.2 dB measured)
     assert s_emu >= 50.0

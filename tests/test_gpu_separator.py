@@ -3,13 +3,18 @@
 * tiny model, a 4-chunk song: the separated audio against the fp32 forward of the oracle, run through
   the same chunk schedule and overlap-add;
 * the full-size model on a 3 s song (one short chunk, 301 frames): audio SNR against the oracle;
+* the full-size model at the reference registry's dim_t = 1700 (749,259-sample chunks) on one chunk:
+  audio SNR against the oracle;
 * the 4:12 synthetic song with the full-size model and 17 s chunks (29 chunks, one batched stack
   forward of 29 x 62 sequences of 1701 frames): identical to the song run in batches of 4 chunks, finite,
-  and the schedule of the reference.
+  and the schedule of the reference; the default batch, sized to the free device memory, covers the song;
+* three threads sharing one Separator get the single-threaded result bit for bit (the reference's
+  tests/test_separator.py:143-157), through ``separate`` and through ``forward_chunks`` on three streams.
 """
 
 from __future__ import annotations
 
+import threading
 import time
 
 import numpy as np
@@ -69,7 +74,7 @@ def test_full_model_short_song_matches_oracle(hip, full_sd):
 def test_full_song_batched(hip, full_sd):
     cfg = weights.RESURRECTION_CFG
     x = signals.song(252.0, seed=7)
-    sep = Separator(full_sd, cfg, 1701, "cuda")
+    sep = Separator(full_sd, cfg, 1701, "cuda", batch_chunks=0)
     assert sep.chunk == 749700 and sep.n_chunks(x.shape[1]) == 29
     print("4:12 song, 29 chunks in one batched stack forward", flush=True)
     sep.separate(x[:, : sep.chunk])  # warm-up (workspace, tables)
@@ -83,3 +88,78 @@ def test_full_song_batched(hip, full_sd):
     out4 = sep4.separate(x)
     assert snr_db(out, out4) >= 60.0
     assert 0.01 < float(np.abs(out).max()) < 10.0
+
+
+def test_full_model_dim_t_1700_matches_oracle(hip, full_sd):
+    """The reference's real chunk length: dim_t = 1700, one 749,259-sample chunk (T = 1700, whose last
+    time-attention key tile is partly masked)."""
+    cfg = weights.RESURRECTION_CFG
+    sep = Separator(full_sd, cfg, weights.RESURRECTION_DIM_T, "cuda")
+    assert sep.chunk == 749259
+    x = signals.song(sep.chunk / 44100, seed=8)
+    assert x.shape[1] == sep.chunk and sep.n_chunks(x.shape[1]) == 1
+    print("full model, dim_t = 1700, one chunk", flush=True)
+    out = sep.separate(x)
+    ref = _oracle_song(x, full_sd, cfg, sep.chunk)
+    s = snr_db(ref, out)
+    print(f"  audio snr vs fp32 oracle {s:.1f} dB")
+    assert s >= 50.0
+
+
+def test_default_batch_fits_device_memory(hip, full_sd):
+    cfg = weights.RESURRECTION_CFG
+    sep = Separator(full_sd, cfg, 1701, "cuda")
+    per = sep.chunk_bytes()
+    free, total = torch.cuda.mem_get_info()
+    b = sep.batch_size(11_113_200)
+    print(f"  {per / 1e9:.2f} GB per chunk, batch of {b} chunks on a {total / 1e9:.0f} GB device")
+    assert 0.6e9 < per < 2.0e9
+    assert 1 <= b and b * per <= total
+    assert Separator(full_sd, cfg, 1701, "cuda", batch_chunks=3).batch_size(11_113_200) == 3
+
+
+def _threaded(n, fn):
+    results = [None] * n
+    errors = []
+
+    def work(i):
+        try:
+            results[i] = fn(i)
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(n)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    return results
+
+
+def test_concurrent_calls_are_serialised(hip, tiny_sd):
+    sep = Separator(tiny_sd, weights.TINY_CFG, weights.TINY_DIM_T, "cuda")
+    x = signals.song(40000 / 44100, seed=14)
+    expected = sep.separate(x)
+    print("3 threads x separate() on one Separator", flush=True)
+    for r in _threaded(3, lambda i: sep.separate(x)):
+        np.testing.assert_array_equal(r, expected)
+
+
+def test_concurrent_forward_chunks_on_three_streams(hip, tiny_sd):
+    """forward_chunks returns device tensors without waiting: each call waits for the previous one's work
+    on the device before it reuses the instance's workspace, whatever stream either ran on."""
+    sep = Separator(tiny_sd, weights.TINY_CFG, weights.TINY_DIM_T, "cuda")
+    chunks = torch.from_numpy(np.stack([signals.song(sep.chunk / 44100, seed=s) for s in (15, 16)]))
+    expected = sep.forward_chunks(chunks).cpu()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+
+    def call(i):
+        with torch.cuda.stream(streams[i]):
+            y = sep.forward_chunks(chunks)
+            streams[i].synchronize()
+            return y.cpu()
+
+    print("3 threads x forward_chunks() on three streams", flush=True)
+    for r in _threaded(3, call):
+        assert torch.equal(r, expected)

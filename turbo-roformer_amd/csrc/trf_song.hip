@@ -3,9 +3,10 @@
 // result / max(weight, 1e-10)).
 //
 // One thread per (channel, sample), in gather form: it finds the chunks that cover its sample (chunk
-// starts are sorted) and adds their terms in ascending chunk order with the same two fp32 roundings per
-// term (product, then sum; no fused multiply-add) as the reference's elementwise ops, so the result is
-// bitwise that of the reference's loop.  A song whose chunks run in several batches accumulates batch
+// starts are sorted; the Python wrapper checks that before uploading them) and adds their terms in
+// ascending chunk order with the same two fp32 roundings per term (product, then sum; no fused
+// multiply-add) as the reference's elementwise ops, so the result is bitwise that of the reference's
+// loop.  A song whose chunks run in several batches accumulates batch
 // after batch into the same sums, which keeps the order.
 #include "trf_device.h"
 
@@ -45,6 +46,9 @@ __global__ __launch_bounds__(256) void k_overlap_add(const float* __restrict__ y
   float ws = ch == 0 ? wsum[i] : 0.f;
   for (int c = c0; c < c1; ++c) {
     const int64_t k = i - starts[c];
+    // Always true for ascending starts; with starts out of order the binary searches can return chunks
+    // that do not cover sample i, and their terms are skipped instead of read out of bounds.
+    if (k < 0 || k >= L) continue;
     const float wk = w[k];
     const float term = y[(int64_t(c) * 2 + ch) * ystride + k] * wk;  // rounded on its own (contract off)
     a = a + term;

@@ -495,16 +495,37 @@ def band_split(feats: torch.Tensor, n_frames: int, dins, packed: torch.Tensor, X
 # ---------------------------------------------------------------------------------------------- song assembly
 
 
-def overlap_add(y: torch.Tensor, L: int, starts: torch.Tensor, window: torch.Tensor, acc: torch.Tensor,
+def check_chunk_starts(starts, nc: int, L: int, n: int) -> list[int]:
+    """The chunk starts of one overlap-add batch as a list of ints, after checking on the host that there
+    are ``nc`` of them, strictly ascending, each chunk's ``L`` samples inside the ``n``-sample song (the
+    kernel finds a sample's chunks by binary search over them).  Raises ValueError."""
+    if isinstance(starts, torch.Tensor):
+        if starts.is_cuda:
+            raise ValueError("starts must be on the host (they are checked before upload)")
+        starts = starts.tolist()
+    starts = [int(s) for s in starts]
+    if len(starts) != nc:
+        raise ValueError(f"starts has {len(starts)} entries for {nc} chunks")
+    if any(b <= a for a, b in zip(starts, starts[1:])):
+        raise ValueError(f"chunk starts must be strictly ascending, got {starts}")
+    if starts and (starts[0] < 0 or starts[-1] + L > n):
+        raise ValueError(f"chunks must lie inside the {n}-sample song (starts {starts[0]}..{starts[-1]}, L = {L})")
+    return starts
+
+
+def overlap_add(y: torch.Tensor, L: int, starts, window: torch.Tensor, acc: torch.Tensor,
                 wsum: torch.Tensor) -> None:
     """acc [2, n] += y[c, :, :L] * window[:L] at starts[c], wsum [n] += window[:L], chunk by chunk in
-    ascending order with the reference's fp32 roundings (chunking.py:39-61). y [nc, 2, Ly] fp32."""
+    ascending order with the reference's fp32 roundings (chunking.py:39-61). y [nc, 2, Ly] fp32.
+
+    ``starts``: the chunks' first samples, a host sequence of ints (or a CPU int tensor).  They are checked
+    here, where they can be read, to be strictly ascending with every chunk's L samples inside the song,
+    then uploaded."""
     lib = load()
     nc = y.shape[0]
     _need(y, "y", torch.float32)
     if y.dim() != 3 or y.shape[1] != 2 or not 1 <= L <= y.shape[2]:
         raise ValueError(f"y must be [chunks, 2, >= L], got {tuple(y.shape)} with L = {L}")
-    _need(starts, "starts", torch.int64, (nc,))
     _need(window, "window", torch.float32)
     if window.numel() < L:
         raise ValueError("window is shorter than L")
@@ -512,7 +533,8 @@ def overlap_add(y: torch.Tensor, L: int, starts: torch.Tensor, window: torch.Ten
     n = acc.shape[1]
     _need(acc, "acc", torch.float32, (2, n))
     _need(wsum, "wsum", torch.float32, (n,))
-    _check(lib.trf_overlap_add(y.data_ptr(), nc, y.shape[2], L, starts.data_ptr(), window.data_ptr(), n,
+    sd = torch.tensor(check_chunk_starts(starts, nc, L, n), dtype=torch.int64).to(acc.device)
+    _check(lib.trf_overlap_add(y.data_ptr(), nc, y.shape[2], L, sd.data_ptr(), window.data_ptr(), n,
                                acc.data_ptr(), wsum.data_ptr(), _stream()))
 
 

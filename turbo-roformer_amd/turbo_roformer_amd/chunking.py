@@ -111,7 +111,7 @@ def overlap_add_device(
         group = starts[b0 : b0 + per]
         y = run(torch.stack([x[:, s : s + C] for s in group]).contiguous()).float().contiguous()
         L = min(C, y.shape[-1])
-        _hip.overlap_add(y, L, torch.tensor(group, dtype=torch.int64, device=dev), w, acc, wsum)
+        _hip.overlap_add(y, L, group, w, acc, wsum)
         if progress is not None:
             for k in range(len(group)):
                 progress(b0 + k + 1, len(starts))

@@ -128,10 +128,17 @@ class HipStack:
         """Free the cached workspace (re-created on the next call)."""
         self._ws = None
 
-    def forward(self, X: torch.Tensor, batch: int, T: int, F: int, events: list | None = None) -> torch.Tensor:
+    def forward(self, X: torch.Tensor, batch: int, T: int, F: int, events: list | None = None,
+                check_finite: bool = False) -> torch.Tensor:
         """Run all sub-layers on X [batch*T*F, 256] fp32 (token order (c, t, f)) in place and return it.
 
+        X must be finite: a NaN or inf token gives non-finite outputs for its sequences (every kernel still
+        runs its fixed number of steps, so nothing hangs).  ``check_finite=True`` checks X on the device
+        first and raises ValueError (this waits for the device, so it is off by default; ``Separator``
+        rejects non-finite audio before the STFT instead).
         ``events``: optional per-kernel timing events (see ``_hip.stack_forward``)."""
+        if check_finite and not bool(torch.isfinite(X).all()):
+            raise ValueError("X contains NaN or inf")
         _hip.stack_forward(
             X, batch, T, F, self.layers, self.modes, self.table(0, T), self.table(1, F), self.workspace(batch, T, F),
             events, self.precision,
