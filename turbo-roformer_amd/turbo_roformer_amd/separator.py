@@ -98,7 +98,7 @@ class Separator:
     ``"fp32"``, mapped to a stack arithmetic by ``REFERENCE_PRECISIONS``; ``stack_precision``: a
     ``HipStack`` precision (``"ff_fp16"``, ``"ff_split"``, ``"bf16"``) that overrides the mapping;
     ``mask_precision``: ``"split"`` or ``"fp16"`` (see ``HipMaskHead``); ``batch_chunks``:
-    chunks per batched stack forward: None (default) sizes batches to the free device memory (about 1.2 GB
+    chunks per batched stack forward: None (default) sizes batches to the free device memory (about 0.9 GB
     per 17 s chunk), 0 runs the whole song at once, k > 0 runs k at a time.
     ``backend``: ``"hip"`` or ``"auto"``; both raise ``HipUnavailable`` when the kernels cannot run, ``"auto"``
     after a warning (this package has no CPU path; ``resolve_backend`` is the non-raising check).
