@@ -10,7 +10,9 @@
  * that follows it (fast.py:377-387), plus the overlap-add that assembles a song from its chunks.
  * Every entry point takes plain device pointers, sizes and a HIP stream;
  * no torch type appears in a signature.  The library allocates no memory and keeps
- * no state beyond a thread-local error string: the caller owns every buffer.
+ * no state beyond a thread-local error string: the caller owns every buffer.  The one
+ * exception is trf_stack_forward_static, whose workspace is a static device array the
+ * library holds on each GPU it runs on (TRF_STATIC_WORKSPACE_BYTES).
  *
  * Shapes are fixed by the model: dim 256, 8 heads x 64, FF hidden 1024 (the mask head's
  * band widths and hidden size are arguments).
@@ -43,7 +45,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 5
+#define TRF_ABI_VERSION 6
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -175,6 +177,24 @@ int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F,
                       const void* const* packed_layers, const int32_t* modes, int32_t n_layers,
                       int32_t precision, const float* rope_time, const float* rope_freq,
                       void* workspace, size_t workspace_bytes, trf_stream_t stream);
+
+/* Size of the static workspace of trf_stack_forward_static: one 17 s chunk (batch 1 at 62 bands, up to
+ * T = 1826 frames; trf_stack_workspace_bytes(1, 1701, 62) is 477 MiB). */
+#define TRF_STATIC_WORKSPACE_BYTES ((size_t)512 << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  trf_stack_forward with the same
+ * kernels and results, but with its workspace in a static device array of TRF_STATIC_WORKSPACE_BYTES
+ * that the library holds on each GPU it runs on until the process ends (its device address is looked up
+ * once per device, on the first call with that device current).  It allocates nothing; shapes whose
+ * trf_stack_workspace_bytes exceed the array fail with TRF_ERR_WORKSPACE.  All calls on one GPU share
+ * that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (other streams
+ * or threads) race, so the caller serialises them.  Nothing in the array has to start at zero: every
+ * workspace element a call reads, the same call wrote first. */
+int trf_stack_forward_static(float* X, int32_t batch, int32_t T, int32_t F,
+                             const void* const* packed_layers, const int32_t* modes, int32_t n_layers,
+                             int32_t precision, const float* rope_time, const float* rope_freq,
+                             trf_stream_t stream);
 
 /* Kernel slots of one layer in launch order (for trf_stack_forward_timed): the QKV GEMM, the
  * attention, and the fused post-attention kernel (out-projection + residual + norm + FF1 + GELU +

@@ -288,6 +288,20 @@ int band_layout(const int32_t* dins, int32_t n_bands, std::vector<size_t>& wofs,
 
 }  // namespace
 
+namespace trf {
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+}  // namespace trf
+
 extern "C" {
 
 int trf_abi_version(void) { return TRF_ABI_VERSION; }

@@ -70,6 +70,9 @@ inline SeqShape seq_shape(int mode, int batch, int T, int F) {
   return s;
 }
 
+// Sets the calling thread's trf_last_error message (printf format) and returns code (trf_capi.hip).
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
 // Kernel launchers (trf_kernels.hip).  They only enqueue work; the caller checks errors.
 // Pack W [rows][K] bf16 into MFMA A-operand tiles (layout: PackLayout); W == nullptr packs zeros.
 void launch_pack(const uint16_t* W, int rows, int K, int layout, uint8_t* dst, hipStream_t st);

@@ -21,7 +21,8 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 5
+ABI_VERSION = 6
+STATIC_WORKSPACE_BYTES = 512 << 20  # TRF_STATIC_WORKSPACE_BYTES of trf_hip.h
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
 MODE_TIME, MODE_FREQ = 0, 1
@@ -90,6 +91,10 @@ _SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P,
          _SZ, ctypes.POINTER(ctypes.c_void_p), _I32, _P],
+    ),
+    "trf_stack_forward_static": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int32), _I32, _I32, _P, _P, _P],
     ),
     "trf_attn_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _P, _SZ, _P]),
     "trf_ff_block": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _I32, _P, _SZ, _P]),
@@ -379,6 +384,33 @@ def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], 
         lib.trf_stack_forward_timed(
             X.data_ptr(), batch, T, F, ptrs, mds, len(layers), prec, _ptr(rope_time), _ptr(rope_freq),
             ws.data_ptr(), ws.numel(), evs, len(handles), _stream(),
+        )
+    )
+
+
+def stack_forward_static(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], rope_time, rope_freq,
+                         precision: str = "ff_fp16") -> None:
+    """``stack_forward`` with the library's static device workspace (``trf_stack_forward_static``): no
+    workspace argument and no device allocation, for callers that cannot allocate.  Calls on one GPU
+    share that workspace, so they must not overlap; shapes whose workspace exceeds
+    ``STATIC_WORKSPACE_BYTES`` raise."""
+    lib = load()
+    prec = precision_code(precision)
+    _need(X, "X", torch.float32, (batch * T * F, DIM))
+    nb = lib.trf_layer_packed_bytes()
+    for i, t in enumerate(layers):
+        _need(t, f"layers[{i}]", torch.uint8, (nb,))
+    if len(modes) != len(layers):
+        raise ValueError("modes and layers differ in length")
+    if any(m == MODE_TIME for m in modes):
+        _need(rope_time, "rope_time", torch.float32, (2, T, HEAD_DIM // 2))
+    if any(m == MODE_FREQ for m in modes):
+        _need(rope_freq, "rope_freq", torch.float32, (2, F, HEAD_DIM // 2))
+    ptrs = (ctypes.c_void_p * max(1, len(layers)))(*[t.data_ptr() for t in layers])
+    mds = (ctypes.c_int32 * max(1, len(modes)))(*modes)
+    _check(
+        lib.trf_stack_forward_static(
+            X.data_ptr(), batch, T, F, ptrs, mds, len(layers), prec, _ptr(rope_time), _ptr(rope_freq), _stream(),
         )
     )
 
