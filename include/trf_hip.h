@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 6
+#define TRF_ABI_VERSION 7
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -148,6 +148,15 @@ int trf_qkv_rope_gemm(const uint16_t* xn, const void* packed_layer, const float*
 int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
                   uint16_t* O, int32_t mode, int32_t batch, int32_t T, int32_t F,
                   trf_stream_t stream);
+
+/* trf_qkv_rope_gemm followed by trf_attention in one kernel, for sequences of at most 64 positions
+ * (L = T in mode 0, F in mode 1; the frequency attention of 62 bands): xn [ntok][256] bf16 -> O
+ * [ntok][512] bf16 with the same arithmetic (shift = the row max), but Q, K, V and the gates never
+ * leave the chip, so no sequence buffers are needed.  The stack uses it for every sub-layer with
+ * L <= 64.  Replaces qkv_rope_gemm + attention (kernels.cpp:439-540, 250-388) for short sequences;
+ * TRF_ERR_ARG when L > 64. */
+int trf_qkv_attention_short(const uint16_t* xn, const void* packed_layer, const float* rope, int32_t mode,
+                            int32_t batch, int32_t T, int32_t F, uint16_t* O, trf_stream_t stream);
 
 /* X += A @ W^T (+ bias); xn = X / max(|X|, eps) as bf16.  which = 0: out-projection
  * (A = O [n][512], no bias); which = 1: FF2 (A = H [n][1024], bias b_ff2).

@@ -1,0 +1,97 @@
+"""The fused QKV + rotary + gates + attention kernel for sequences of at most 64 positions
+(``trf_qkv_attention_short``, used by the stack for frequency attention) against the oracle's emulation
+of the reference's two ops (qkv_rope_gemm, then attention: kernels.cpp:439-540, 250-388), and against the
+library's unfused pair on the same inputs.
+
+Shapes: the 62-band frequency attention (batched, up to the 300-frame chunk), 64 and 33 positions, one
+position, and time attention of chunks of at most 64 frames.  The q and k rows of the weights are scaled up so
+that the scores span tens of units (peaked softmax rows).  Tolerance: the per-op bar of the unfused
+kernels (two bf16 steps elementwise, one rounding flip in 1e-4 of the elements, SNR floor), and every
+output token written.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import folded, kernels as ok
+from turbo_roformer_amd import _hip, weights
+from turbo_roformer_amd.stack import rope_table
+
+from .conftest import assert_bf16_close, rand_x, snr_db
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+SHAPES = [  # (mode, batch, T, F)
+    (1, 1, 300, 62),
+    (1, 2, 37, 62),
+    (1, 3, 11, 64),
+    (1, 1, 9, 33),
+    (1, 1, 5, 1),
+    (1, 1, 100, 7),
+    (0, 1, 64, 3),
+    (0, 1, 40, 5),
+    (0, 2, 1, 5),
+]
+
+
+@pytest.fixture(scope="module")
+def sharp_layers(hip):
+    """(bf16 weights, packed layer) of a time and a freq sub-layer with the q and k rows scaled by 6."""
+    cfg = dict(weights.TINY_CFG, depth=1)
+    sd = weights.init_state_dict(cfg, seed=5, init="normal")
+    out = []
+    for P in folded.fold(sd, 1):
+        w = ok.bf16_weights(P)
+        W = w["W"].float().clone()
+        W[:1024] *= 6.0
+        w["W"] = W.to(torch.bfloat16)
+        packed = torch.empty(_hip.layer_packed_bytes(), dtype=torch.uint8, device=DEV)
+        _hip.pack_layer(w["W"].to(DEV), w["b_gate"].to(DEV), w["Wo"].to(DEV), w["W1"].to(DEV), w["b1"].to(DEV),
+                        w["W2"].to(DEV), w["b2"].to(DEV), out=packed)
+        out.append((w, packed))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("mode,batch,T,F", SHAPES)
+def test_fused_short_attention(sharp_layers, mode, batch, T, F):
+    w, packed = sharp_layers[mode]
+    n = batch * T * F
+    L = T if mode == 0 else F
+    xn = ok.l2_rows(rand_x(n, 40 + T + F)).to(torch.bfloat16)
+    Q, K, Vt, G = ok.qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], mode, batch, T, F)
+    Oref = ok.attention(Q, K, Vt, G, mode, batch, T, F)
+    xd = xn.to(DEV)
+    rope = rope_table(w["freqs"], L).to(DEV)
+    O = torch.full((n, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
+    print(f"fused short attention mode={mode} batch={batch} T={T} F={F}", flush=True)
+    _hip.qkv_attention_short(xd, packed, rope, mode, batch, T, F, O)
+    # the library's unfused pair on the same inputs
+    Qd, Kd, Vd, Gd = _hip.seq_buffers(mode, batch, T, F)
+    O2 = torch.empty(n, 512, dtype=torch.bfloat16, device=DEV)
+    _hip.qkv_rope_gemm(xd, packed, rope, mode, batch, T, F, Qd, Kd, Vd, Gd)
+    _hip.attention(Qd, Kd, Vd, Gd, O2, mode, batch, T, F)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O.float()).all(), "every token's output is written"
+    assert_bf16_close(Oref, O, "O fused", min_snr=48)
+    s_pair = snr_db(O2.double().cpu().numpy(), O.double().cpu().numpy())
+    same = float((O == O2).float().mean())
+    print(f"  vs oracle {snr_db(Oref.double().numpy(), O.double().cpu().numpy()):.1f} dB, vs unfused pair "
+          f"{s_pair:.1f} dB ({100 * same:.2f}% bitwise equal)")
+    assert s_pair >= 55.0
+
+
+def test_fused_short_attention_rejects_long_sequences(sharp_layers):
+    w, packed = sharp_layers[1]
+    xn = torch.zeros(65 * 2, 256, dtype=torch.bfloat16, device=DEV)
+    O = torch.empty(65 * 2, 512, dtype=torch.bfloat16, device=DEV)
+    rope = rope_table(w["freqs"], 65).to(DEV)
+    with pytest.raises(ValueError):
+        _hip.qkv_attention_short(xn, packed, rope, 1, 1, 2, 65, O)
+    lib = _hip.load()
+    assert lib.trf_qkv_attention_short(xn.data_ptr(), packed.data_ptr(), rope.data_ptr(), 1, 1, 2, 65,
+                                       O.data_ptr(), None) == 1
+    assert "at most 64" in lib.trf_last_error().decode()

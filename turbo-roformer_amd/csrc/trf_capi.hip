@@ -118,18 +118,28 @@ struct Events {
     if (int rc_ = (expr)) return rc_; \
   } while (0)
 
-// One sub-layer on an already normalised xn: qkv + rotary, attention, then the fused out-proj +
-// residual + norm, and (with_ff) FF1 + GELU + FF2 + residual + norm in the same kernel.
+// One sub-layer on an already normalised xn: qkv + rotary, attention (one fused kernel for sequences of
+// at most 64 positions, whose time goes to the attention slot), then the fused out-proj + residual +
+// norm, and (with_ff) FF1 + GELU + FF2 + residual + norm in the same kernel.
 int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
               int64_t n, bool with_ff, int ff_precision, hipStream_t st, const Events& ev = Events{}) {
-  TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
-  trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
-  TRF_TRY(check_launch("qkv_rope_gemm"));
-  TRF_TRY(ev.record(TRF_SLOT_QKV, 1, st));
-  TRF_TRY(ev.record(TRF_SLOT_ATTN, 0, st));
-  trf::launch_attention(w.Q, w.K, w.Vt, w.G, w.O, sh, st);
-  TRF_TRY(check_launch("attention"));
-  TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
+  if (sh.L <= 64) {
+    TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
+    TRF_TRY(ev.record(TRF_SLOT_QKV, 1, st));
+    TRF_TRY(ev.record(TRF_SLOT_ATTN, 0, st));
+    trf::launch_qkv_attn_short(w.xn, layer, rope, sh, w.O, st);
+    TRF_TRY(check_launch("qkv_attention_short"));
+    TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
+  } else {
+    TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
+    trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
+    TRF_TRY(check_launch("qkv_rope_gemm"));
+    TRF_TRY(ev.record(TRF_SLOT_QKV, 1, st));
+    TRF_TRY(ev.record(TRF_SLOT_ATTN, 0, st));
+    trf::launch_attention(w.Q, w.K, w.Vt, w.G, w.O, sh, st);
+    TRF_TRY(check_launch("attention"));
+    TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
+  }
   TRF_TRY(ev.record(TRF_SLOT_POST, 0, st));
   trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, ff_precision, 1e-12f, st);
   TRF_TRY(check_launch("post_attention"));
@@ -389,6 +399,20 @@ int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, cons
   const trf::SeqShape sh = trf::seq_shape(mode, batch, T, F);
   trf::launch_attention(Q, K, Vt, G, O, sh, as_hip(stream));
   return check_launch("attention");
+}
+
+int trf_qkv_attention_short(const uint16_t* xn, const void* packed_layer, const float* rope, int32_t mode,
+                            int32_t batch, int32_t T, int32_t F, uint16_t* O, trf_stream_t stream) {
+  if (int rc = check_mode(mode)) return rc;
+  if (int rc = check_shape(batch, T, F)) return rc;
+  const trf::SeqShape sh = trf::seq_shape(mode, batch, T, F);
+  if (sh.L > 64) return fail(TRF_ERR_ARG, "sequences of %d positions: the fused kernel takes at most 64", sh.L);
+  TRF_REQUIRE(xn, "xn");
+  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(rope, "rope");
+  TRF_REQUIRE(O, "O");
+  trf::launch_qkv_attn_short(xn, static_cast<const uint8_t*>(packed_layer), rope, sh, O, as_hip(stream));
+  return check_launch("qkv_attention_short");
 }
 
 int trf_gemm_res_norm(const uint16_t* A, const void* packed_layer, int32_t which, float* X, uint16_t* xn,

@@ -60,6 +60,22 @@ __device__ __forceinline__ u32x4 zero4() {
 // Feature offset of accumulator register group g (registers 4g..4g+3) of a 32-row tile.
 __device__ __forceinline__ int row_of_group(int g, int hh) { return 8 * g + 4 * hh; }
 
+// Token index of position p in sequence s (see the token-order contract in trf_hip.h).
+__device__ __forceinline__ int64_t token_of(int mode, int s, int p, int T, int F) {
+  if (mode == 0) {
+    const int c = s / F, f = s - c * F;
+    return (int64_t(c) * T + p) * F + f;
+  }
+  return int64_t(s) * F + p;
+}
+
+// max of x over lanes l and l ^ 32: v_permlane32_swap exchanges the half-waves, so of its two results
+// one is x and the other the partner's value, in either order.
+__device__ __forceinline__ float halfwave_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Index of this wave in the workgroup, as a scalar (uniform) value so that addresses derived from it
 // stay in scalar registers.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }

@@ -85,6 +85,10 @@ void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, con
                 uint16_t* Q, uint16_t* K, uint16_t* Vt, float* G, hipStream_t st);
 void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
                       uint16_t* O, const SeqShape& sh, hipStream_t st);
+// Fused QKV + rotary + gates + attention for sequences of at most 64 positions (trf_qkv_attn_short.hip):
+// xn -> O with no Q/K/V/G buffers.  Requires sh.L <= 64.
+void launch_qkv_attn_short(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
+                           uint16_t* O, hipStream_t st);
 void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
                           int64_t n, float eps, hipStream_t st);
 void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);

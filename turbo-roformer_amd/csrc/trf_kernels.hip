@@ -17,15 +17,6 @@
 
 namespace trf {
 
-// Token index of position p in sequence s (see the token-order contract in trf_hip.h).
-__device__ __forceinline__ int64_t token_of(int mode, int s, int p, int T, int F) {
-  if (mode == 0) {
-    const int c = s / F, f = s - c * F;
-    return (int64_t(c) * T + p) * F + f;
-  }
-  return int64_t(s) * F + p;
-}
-
 // ============================================================ weight packing
 // 32x32 layouts: dst[t][ks][lane][e] = W[32t + lane%32][16ks + kperm(lane/32, e)] (kperm: natural 8hh + e,
 // or register order 4hh + e / 8 + 4hh + e - 4).  16x16 layouts: dst[t][ks][lane][e] =
@@ -443,13 +434,6 @@ __device__ __forceinline__ void load_k_half(const u32x4* __restrict__ Kl, int kh
 constexpr float kAttHeadroom = 8.0f;       // guarded sweep
 constexpr float kAttHeadroomFast = 32.0f;  // fixed-shift sweep
 constexpr float kAttSafeSum = 1099511627776.0f;  // 2^40: fixed-shift sums at most this leave O finite
-
-// max of x over lanes l and l ^ 32: v_permlane32_swap exchanges the half-waves, so of its two results
-// one is x and the other the partner's value, in either order.
-__device__ __forceinline__ float halfwave_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
 
 // One 32-key half of a tile for one 32-query column tile: S^T = K.Q^T accumulated onto -c, then
 // P = 2^(s - c) as two B operands and the fp32 sum.  FIRST (the first half of tile 0, 32 valid keys) sets c

@@ -21,7 +21,7 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 6
+ABI_VERSION = 7
 STATIC_WORKSPACE_BYTES = 512 << 20  # TRF_STATIC_WORKSPACE_BYTES of trf_hip.h
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
@@ -79,6 +79,7 @@ _SIGNATURES: dict[str, tuple] = {
     "trf_add_rmsnorm": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I64, _F, _P]),
     "trf_qkv_rope_gemm": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
     "trf_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
+    "trf_qkv_attention_short": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P]),
     "trf_gemm_res_norm": (ctypes.c_int, [_P, _P, _I32, _P, _P, _I64, _F, _P]),
     "trf_gemm_gelu": (ctypes.c_int, [_P, _P, _P, _I64, _P]),
     "trf_stack_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
@@ -313,6 +314,22 @@ def attention(Q, K, Vt, G, O, mode, batch, T, F) -> None:
     _need(G, "G", torch.float32, (n, HEADS))
     _need(O, "O", torch.bfloat16, (n, HEADS * HEAD_DIM))
     _check(lib.trf_attention(Q.data_ptr(), K.data_ptr(), Vt.data_ptr(), G.data_ptr(), O.data_ptr(), mode, batch, T, F, _stream()))
+
+
+def qkv_attention_short(xn, layer, rope, mode, batch, T, F, O) -> None:
+    """``qkv_rope_gemm`` + ``attention`` fused for sequences of at most 64 positions: xn [ntok, 256] bf16
+    -> O [ntok, 512] bf16, no sequence buffers."""
+    lib = load()
+    nseq, L, Lp = seq_shape(mode, batch, T, F)
+    if L > 64:
+        raise ValueError(f"sequences of {L} positions: the fused kernel takes at most 64")
+    n = batch * T * F
+    _need(xn, "xn", torch.bfloat16, (n, DIM))
+    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    _need(rope, "rope", torch.float32, (2, L, HEAD_DIM // 2))
+    _need(O, "O", torch.bfloat16, (n, HEADS * HEAD_DIM))
+    _check(lib.trf_qkv_attention_short(xn.data_ptr(), layer.data_ptr(), rope.data_ptr(), mode, batch, T, F,
+                                       O.data_ptr(), _stream()))
 
 
 def gemm_res_norm(A, layer, which, X, xn, eps: float = 1e-12) -> None:
