@@ -162,45 +162,79 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
+    def slot_names(mode: int) -> dict[int, str]:
+        """Kernel of each slot of a sub-layer: sequences of at most 64 positions (frequency attention at
+        62 bands) run QKV and attention as one fused kernel, reported in the attention slot."""
+        L = T if mode == 0 else F
+        if L <= 64:
+            return {1: "qkv_attention_short", 2: "post_attention"}
+        return {0: "qkv_rope_gemm", 1: "attention", 2: "post_attention"}
+
+    def make_events(stack, steps: int, want) -> list:
+        """Per step, the trf_stack_forward_timed event list: an Event pair for each (layer, slot) that
+        want(mode, slot) selects, None elsewhere (the library records nothing for None)."""
+        nslot = len(_hip.SLOTS)
+        out = []
+        for _ in range(steps):
+            evs = [None] * (2 * nslot * len(stack.layers))
+            for i, mode in enumerate(stack.modes):
+                for sl in slot_names(mode):
+                    if want(mode, sl):
+                        evs[2 * (i * nslot + sl)] = torch.cuda.Event(enable_timing=True)
+                        evs[2 * (i * nslot + sl) + 1] = torch.cuda.Event(enable_timing=True)
+            for e in evs:  # create the underlying events outside the timed region
+                if e is not None:
+                    e.record()
+            out.append(evs)
+        torch.cuda.synchronize()
+        return out
+
+    def per_kernel_ms(stack, events) -> dict[str, float]:
+        nslot = len(_hip.SLOTS)
+        acc: dict[str, list[float]] = {}
+        for evs in events:
+            for i, mode in enumerate(stack.modes):
+                for sl, name in slot_names(mode).items():
+                    e0, e1 = evs[2 * (i * nslot + sl)], evs[2 * (i * nslot + sl) + 1]
+                    if e0 is not None:
+                        acc.setdefault(f"{name}_{'t' if mode == 0 else 'f'}", []).append(e0.elapsed_time(e1))
+        return {k: float(np.mean(v)) for k, v in acc.items()}
+
     def timed(precision: str, with_events: bool):
-        """(ms per stack forward, per-kernel ms or None, output) for one precision."""
+        """(ms per stack forward, per-kernel ms or None, time-attention ms or None, output) for one
+        precision.  In the timed forwards only the time-attention kernels (the roofline kernel) carry
+        events, attached to their dispatch; the per-kernel table comes from as many forwards after them,
+        with events on every kernel (each event pair adds a few microseconds between kernels)."""
         stack = HipStack(sd, "cuda", precision=precision)
         X = torch.empty_like(Xd0)
-        nslot = len(_hip.SLOTS)
         for _ in range(a.warmup):
             X.copy_(Xd0)
             stack(X, 1, T, F)
         torch.cuda.synchronize()
-        events = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nslot * len(stack.layers))]
-                  for _ in range(a.steps)] if with_events else [None] * a.steps
-        for evs in events:  # create the underlying events outside the timed region
-            for e in evs or ():
-                e.record()
-        torch.cuda.synchronize()
+        timed_events = make_events(stack, a.steps, lambda mode, sl: with_events and mode == 0 and sl == 1)
         t0 = time.perf_counter()
         for k in range(a.steps):
             X.copy_(Xd0)
-            stack(X, 1, T, F, events=events[k])
+            stack(X, 1, T, F, events=timed_events[k] if with_events else None)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         ms = (t1 - t0) * 1e3 / a.steps
         print(f"bench: {a.steps} timed stack forwards ({precision}), {ms:.3f} ms each", file=sys.stderr, flush=True)
-        kernel_ms = None
-        if with_events:
-            per_kernel: dict[str, list[float]] = {}
-            for evs in events:
-                for i, mode in enumerate(stack.modes):
-                    for sl, name in enumerate(_hip.SLOTS):
-                        key = f"{name}_{'t' if mode == 0 else 'f'}"
-                        dt = evs[2 * (i * nslot + sl)].elapsed_time(evs[2 * (i * nslot + sl) + 1])
-                        per_kernel.setdefault(key, []).append(dt)
-            kernel_ms = {k: float(np.mean(v)) for k, v in per_kernel.items()}
+        kernel_ms = attn_ms = None
         out = X.view(1, T, F, 256).cpu()
+        if with_events:
+            attn_ms = per_kernel_ms(stack, timed_events)["attention_t"]
+            prof_events = make_events(stack, a.steps, lambda mode, sl: True)
+            for k in range(a.steps):
+                X.copy_(Xd0)
+                stack(X, 1, T, F, events=prof_events[k])
+            torch.cuda.synchronize()
+            kernel_ms = per_kernel_ms(stack, prof_events)
         del stack, X
         torch.cuda.empty_cache()
-        return ms, kernel_ms, out
+        return ms, kernel_ms, attn_ms, out
 
-    ms, kernel_ms, out_gpu = timed(a.precision, True)
+    ms, kernel_ms, attn_t_ms, out_gpu = timed(a.precision, True)
     alts = {p: timed(p, False) for p in ("ff_fp16", "ff_split", "bf16") if p != a.precision}
 
     # the mask head after the stack, on this chunk's stack output (HIP events on its launch stream)
@@ -226,7 +260,6 @@ def main() -> int:
                    "gflop_per_chunk": round(mask_flops / 1e9, 2),
                    "tflops": round(mask_flops / (mask_ms * 1e-3) / 1e12, 1)}
     del xg, mask_buf
-    attn_t_ms = kernel_ms["attention_t"]
     flops_t = attn_flops(F, T)
     achieved = flops_t / (attn_t_ms * 1e-3) / 1e12
 
@@ -322,7 +355,7 @@ def main() -> int:
         # the product path: HIP stack, then the HIP mask head
         m_gpu = mask_of(out_gpu)
         snr_mask = signals.snr_db(m_ref.numpy(), m_gpu.numpy())
-        snr_alts = {p: signals.snr_db(m_ref.numpy(), mask_of(v[2]).numpy()) for p, v in alts.items()}
+        snr_alts = {p: signals.snr_db(m_ref.numpy(), mask_of(v[3]).numpy()) for p, v in alts.items()}
         result["mask_head"]["cpu_ms_per_chunk"] = round(mask_cpu_s * 1e3, 1)
         result["mask_head"]["cpu_sample"] = f"oracle fp32 mask estimator on {threads} threads, one chunk"
         # the head alone: HIP mask head on the fp32 stack output against the fp32 mask estimator

@@ -215,10 +215,13 @@ enum trf_kernel_slot {
   TRF_SLOTS_PER_LAYER = 3
 };
 
-/* trf_stack_forward that also records caller-created hipEvent_t handles around kernels:
- * events[2*(i*TRF_SLOTS_PER_LAYER + k)] before and events[... + 1] after kernel k of layer i,
- * skipping NULL entries; n_events must be 0 or 2*TRF_SLOTS_PER_LAYER*n_layers.  This is the
- * counterpart of the reference's per-section wall-clock profile (fast.py:62-80, 279-340). */
+/* trf_stack_forward that also records caller-created hipEvent_t handles at the start and end of each
+ * kernel: events[2*(i*TRF_SLOTS_PER_LAYER + k)] and events[... + 1] for kernel k of layer i, skipping
+ * NULL entries; n_events must be 0 or 2*TRF_SLOTS_PER_LAYER*n_layers.  The events are part of the
+ * kernel's dispatch (hipExtLaunchKernel), which costs less than separate event records; a layer with
+ * sequences of at most 64 positions has one kernel for QKV and attention, reported in the attention
+ * slot, and its QKV slot is an empty interval.  This is the counterpart of the reference's
+ * per-section wall-clock profile (fast.py:62-80, 279-340). */
 int trf_stack_forward_timed(float* X, int32_t batch, int32_t T, int32_t F,
                             const void* const* packed_layers, const int32_t* modes,
                             int32_t n_layers, int32_t precision, const float* rope_time,

@@ -112,3 +112,34 @@ def test_full_size_axial_equivariance(full_stack, layer, axis):
     a = Xa.view(1, T, F, 256).cpu().index_select(axis, perm)
     assert torch.equal(a, Xb.view(1, T, F, 256).cpu())
     assert torch.isfinite(a).all()
+
+
+def test_timed_forward_equals_untimed_and_times_each_kernel(hip, tiny_sd):
+    """trf_stack_forward_timed attaches caller events to the kernels' dispatches: the result is the untimed
+    forward's bit for bit, every requested kernel gets a positive duration, None entries record nothing,
+    and the QKV slot of a sub-layer with at most 64 positions (one fused kernel) is an empty interval."""
+    from turbo_roformer_amd import _hip
+
+    stack = HipStack(tiny_sd, DEV)
+    _, X = _tokens(tiny_sd, weights.TINY_HOP * 99, seed=9)  # T = 100 frames (time: two kernels), F = 29 (fused)
+    b, T, F, _ = X.shape
+    Xa = X.reshape(-1, 256).contiguous().to(DEV)
+    Xb = Xa.clone()
+    nslot, n = len(_hip.SLOTS), len(stack.layers)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * nslot * n)]
+    events[2 * (1 * nslot + 2)] = events[2 * (1 * nslot + 2) + 1] = None  # layer 1's post-attention: untimed
+    print(f"timed stack forward T={T} F={F}", flush=True)
+    stack(Xa, b, T, F)
+    stack(Xb, b, T, F, events=events)
+    torch.cuda.synchronize()
+    assert torch.equal(Xa, Xb)
+    for i, mode in enumerate(stack.modes):
+        for sl in range(nslot):
+            e0, e1 = events[2 * (i * nslot + sl)], events[2 * (i * nslot + sl) + 1]
+            if e0 is None:
+                continue
+            dt = e0.elapsed_time(e1)
+            if mode == 1 and sl == 0:
+                assert 0.0 <= dt < 0.05  # no kernel of its own
+            else:
+                assert dt > 0.0, (i, sl)

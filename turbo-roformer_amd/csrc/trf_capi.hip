@@ -99,16 +99,27 @@ Workspace plan(int32_t batch, int32_t T, int32_t F, uint8_t* base) {
 
 hipStream_t as_hip(trf_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Optional event pair around each kernel of a layer (profiling); events == nullptr disables it.
+// Optional event pair of each kernel of a layer (profiling): attached to the kernel's dispatch; events ==
+// nullptr, or a NULL entry, records nothing.
 struct Events {
   void* const* ev = nullptr;
   int layer = 0;
-  int record(int slot, int end, hipStream_t st) const {
-    if (!ev) return TRF_OK;
-    void* e = ev[2 * (layer * TRF_SLOTS_PER_LAYER + slot) + end];
-    if (!e) return TRF_OK;
-    const hipError_t rc = hipEventRecord(reinterpret_cast<hipEvent_t>(e), st);
-    if (rc != hipSuccess) return fail(TRF_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(rc));
+  trf::LaunchEvents of(int slot) const {
+    trf::LaunchEvents e;
+    if (ev) {
+      e.start = reinterpret_cast<hipEvent_t>(ev[2 * (layer * TRF_SLOTS_PER_LAYER + slot)]);
+      e.stop = reinterpret_cast<hipEvent_t>(ev[2 * (layer * TRF_SLOTS_PER_LAYER + slot) + 1]);
+    }
+    return e;
+  }
+  // Marks a slot with no kernel of its own as an empty interval (both events, if given, recorded here).
+  int empty(int slot, hipStream_t st) const {
+    const trf::LaunchEvents e = of(slot);
+    for (hipEvent_t x : {e.start, e.stop}) {
+      if (!x) continue;
+      const hipError_t rc = hipEventRecord(x, st);
+      if (rc != hipSuccess) return fail(TRF_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(rc));
+    }
     return TRF_OK;
   }
 };
@@ -124,26 +135,17 @@ struct Events {
 int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
               int64_t n, bool with_ff, int ff_precision, hipStream_t st, const Events& ev = Events{}) {
   if (sh.L <= 64) {
-    TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
-    TRF_TRY(ev.record(TRF_SLOT_QKV, 1, st));
-    TRF_TRY(ev.record(TRF_SLOT_ATTN, 0, st));
-    trf::launch_qkv_attn_short(w.xn, layer, rope, sh, w.O, st);
+    TRF_TRY(ev.empty(TRF_SLOT_QKV, st));
+    trf::launch_qkv_attn_short(w.xn, layer, rope, sh, w.O, st, ev.of(TRF_SLOT_ATTN));
     TRF_TRY(check_launch("qkv_attention_short"));
-    TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
   } else {
-    TRF_TRY(ev.record(TRF_SLOT_QKV, 0, st));
-    trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st);
+    trf::launch_qkv(w.xn, layer, rope, sh, w.Q, w.K, w.Vt, w.G, st, ev.of(TRF_SLOT_QKV));
     TRF_TRY(check_launch("qkv_rope_gemm"));
-    TRF_TRY(ev.record(TRF_SLOT_QKV, 1, st));
-    TRF_TRY(ev.record(TRF_SLOT_ATTN, 0, st));
-    trf::launch_attention(w.Q, w.K, w.Vt, w.G, w.O, sh, st);
+    trf::launch_attention(w.Q, w.K, w.Vt, w.G, w.O, sh, st, ev.of(TRF_SLOT_ATTN));
     TRF_TRY(check_launch("attention"));
-    TRF_TRY(ev.record(TRF_SLOT_ATTN, 1, st));
   }
-  TRF_TRY(ev.record(TRF_SLOT_POST, 0, st));
-  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, ff_precision, 1e-12f, st);
-  TRF_TRY(check_launch("post_attention"));
-  return ev.record(TRF_SLOT_POST, 1, st);
+  trf::launch_post_attn(w.O, layer, X, w.xn, n, with_ff, ff_precision, 1e-12f, st, ev.of(TRF_SLOT_POST));
+  return check_launch("post_attention");
 }
 
 int stack_impl(float* X, int32_t batch, int32_t T, int32_t F, const void* const* packed_layers, const int32_t* modes,

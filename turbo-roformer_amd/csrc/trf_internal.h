@@ -1,6 +1,7 @@
 // Internal declarations shared by the kernel and C-ABI translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -73,6 +74,12 @@ inline SeqShape seq_shape(int mode, int batch, int T, int F) {
 // Sets the calling thread's trf_last_error message (printf format) and returns code (trf_capi.hip).
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// Optional start / stop events of a launch.  hipExtLaunchKernelGGL records them with the dispatch itself,
+// which costs less than separate event-record packets around it (no events: a plain launch).
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
 // Kernel launchers (trf_kernels.hip).  They only enqueue work; the caller checks errors.
 // Pack W [rows][K] bf16 into MFMA A-operand tiles (layout: PackLayout); W == nullptr packs zeros.
 void launch_pack(const uint16_t* W, int rows, int K, int layout, uint8_t* dst, hipStream_t st);
@@ -82,20 +89,20 @@ void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st);
 void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n,
                         float eps, hipStream_t st);
 void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
-                uint16_t* Q, uint16_t* K, uint16_t* Vt, float* G, hipStream_t st);
+                uint16_t* Q, uint16_t* K, uint16_t* Vt, float* G, hipStream_t st, const LaunchEvents& ev = {});
 void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
-                      uint16_t* O, const SeqShape& sh, hipStream_t st);
+                      uint16_t* O, const SeqShape& sh, hipStream_t st, const LaunchEvents& ev = {});
 // Fused QKV + rotary + gates + attention for sequences of at most 64 positions (trf_qkv_attn_short.hip):
 // xn -> O with no Q/K/V/G buffers.  Requires sh.L <= 64.
 void launch_qkv_attn_short(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
-                           uint16_t* O, hipStream_t st);
+                           uint16_t* O, hipStream_t st, const LaunchEvents& ev = {});
 void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
                           int64_t n, float eps, hipStream_t st);
 void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);
 // Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm]; ff_precision is a
 // FfPrecision value for the two FF GEMMs.
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
-                      int ff_precision, float eps, hipStream_t st);
+                      int ff_precision, float eps, hipStream_t st, const LaunchEvents& ev = {});
 // Fused FF1 + GELU + FF2 + residual + norm on X (updated in place, its norm computed in the kernel);
 // xn is written as X / |X|.
 void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, int ff_precision, float eps, hipStream_t st);

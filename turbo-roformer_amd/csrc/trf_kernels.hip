@@ -287,10 +287,10 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
 }
 
 void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh, uint16_t* Q,
-                uint16_t* K, uint16_t* Vt, float* G, hipStream_t st) {
+                uint16_t* K, uint16_t* Vt, float* G, hipStream_t st, const LaunchEvents& ev) {
   const int64_t rows = int64_t(sh.nseq) * sh.Lpad;
   const unsigned blocks = unsigned((rows / 32 + kQkvWaves - 1) / kQkvWaves);
-  hipLaunchKernelGGL(k_qkv_rope, dim3(blocks), dim3(64 * kQkvWaves), 0, st, xn,
+  hipExtLaunchKernelGGL(k_qkv_rope, dim3(blocks), dim3(64 * kQkvWaves), 0, st, ev.start, ev.stop, 0, xn,
                      reinterpret_cast<const u32x4*>(layer + kOffQkvg),
                      reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.Lpad,
                      sh.T, sh.F, Q, K, Vt, G);
@@ -676,14 +676,16 @@ __global__ __launch_bounds__(256) void k_attn_short(const uint16_t* __restrict__
 }
 
 void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G, uint16_t* O,
-                      const SeqShape& sh, hipStream_t st) {
+                      const SeqShape& sh, hipStream_t st, const LaunchEvents& ev) {
   if (sh.L <= 64) {
     const int nsh = sh.nseq * kHeads;
-    hipLaunchKernelGGL(k_attn_short, dim3((nsh + 3) / 4), dim3(256), 0, st, Q, K, Vt, G, O, sh.mode, nsh, sh.L,
+    hipExtLaunchKernelGGL(k_attn_short, dim3((nsh + 3) / 4), dim3(256), 0, st, ev.start, ev.stop, 0, Q, K, Vt, G, O,
+                          sh.mode, nsh, sh.L,
                        sh.T, sh.F);
   } else {
     const int nqb = (sh.L + kAttBlockQ - 1) / kAttBlockQ;
-    hipLaunchKernelGGL(k_attn_long, dim3(sh.nseq * kHeads * nqb), dim3(64 * kAttWaves), 0, st, Q, K, Vt, G, O,
+    hipExtLaunchKernelGGL(k_attn_long, dim3(sh.nseq * kHeads * nqb), dim3(64 * kAttWaves), 0, st, ev.start, ev.stop,
+                          0, Q, K, Vt, G, O,
                        sh.mode, sh.L, sh.Lpad, sh.T, sh.F, nqb);
   }
 }
@@ -1325,19 +1327,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,
-                      int ff_precision, float eps, hipStream_t st) {
+                      int ff_precision, float eps, hipStream_t st, const LaunchEvents& ev) {
   if (with_ff && ff_precision == kFfSplit) {
     const unsigned blocks = unsigned((n + 16 * kX3Waves - 1) / (16 * kX3Waves));
-    hipLaunchKernelGGL(k_mlp_x3<true>, dim3(blocks), dim3(64 * kX3Waves), 0, st, O, layer, X, xn, n, eps);
+    hipExtLaunchKernelGGL(k_mlp_x3<true>, dim3(blocks), dim3(64 * kX3Waves), 0, st, ev.start, ev.stop, 0, O, layer, X,
+                          xn, n, eps);
     return;
   }
   const unsigned blocks = unsigned((n + 32 * kMlpWaves - 1) / (32 * kMlpWaves));
   if (!with_ff)
-    hipLaunchKernelGGL((k_mlp<true, false, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+    hipExtLaunchKernelGGL((k_mlp<true, false, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, ev.start, ev.stop, 0, O, layer,
+                          X, xn, n, eps);
   else if (ff_precision == kFfFp16)
-    hipLaunchKernelGGL((k_mlp<true, true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+    hipExtLaunchKernelGGL((k_mlp<true, true, true>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, ev.start, ev.stop, 0, O, layer,
+                          X, xn, n, eps);
   else
-    hipLaunchKernelGGL((k_mlp<true, true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, O, layer, X, xn, n, eps);
+    hipExtLaunchKernelGGL((k_mlp<true, true, false>), dim3(blocks), dim3(64 * kMlpWaves), 0, st, ev.start, ev.stop, 0, O, layer,
+                          X, xn, n, eps);
 }
 
 void launch_ff(const uint8_t* layer, float* X, uint16_t* xn, int64_t n, int ff_precision, float eps, hipStream_t st) {

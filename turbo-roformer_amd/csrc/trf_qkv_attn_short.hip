@@ -366,9 +366,9 @@ __global__ __launch_bounds__(256, 1) void k_qkv_attn_short(const uint16_t* __res
 }
 
 void launch_qkv_attn_short(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
-                           uint16_t* O, hipStream_t st) {
+                           uint16_t* O, hipStream_t st, const LaunchEvents& ev) {
   const unsigned blocks = unsigned((sh.nseq + kFsWaves - 1) / kFsWaves);
-  hipLaunchKernelGGL(k_qkv_attn_short, dim3(blocks), dim3(64 * kFsWaves), 0, st, xn,
+  hipExtLaunchKernelGGL(k_qkv_attn_short, dim3(blocks), dim3(64 * kFsWaves), 0, st, ev.start, ev.stop, 0, xn,
                      reinterpret_cast<const u32x4*>(layer + kOffQkvg),
                      reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.T, sh.F, O);
 }
