@@ -117,4 +117,18 @@ __device__ __forceinline__ void stage_barrier() {
   __syncthreads();
 }
 
+// This thread's vector memory operations have completed except the N most recent, then all waves
+// meet.  On gfx9 loads, direct-to-LDS loads and stores share the one vmcnt counter and complete in
+// issue order, so a stage can leave its stores in flight and still wait for exactly the loads issued
+// before them.  The barrier is the bare s_barrier: __syncthreads' release fence would wait for the N
+// younger operations too.  The empty asm statements keep the compiler from moving LDS accesses across.
+template <int N>
+__device__ __forceinline__ void vmcnt_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace trf

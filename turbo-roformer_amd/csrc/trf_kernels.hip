@@ -155,11 +155,18 @@ void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_
 // One wave owns 32 consecutive padded positions of one sequence; its 32 tokens' xn rows stay in
 // registers as B operands.  The workgroup (8 waves, 2 per SIMD) streams the 49 weight tiles through
 // LDS four per stage (13 stages: q heads, k heads, v heads, then the gate tile), so every stage is of
-// one kind and its four MFMA chains run interleaved.  The rotary cos/sin of the wave's position and
-// the gate biases are loaded into registers once.  (kernels.cpp:439-540)
+// one kind.  The rotary cos/sin of the wave's position is loaded into registers once.
+// (kernels.cpp:439-540)
+//
+// A stage runs as two groups of two tiles (two interleaved MFMA chains each).  A group's outputs
+// leave as 8 packed 8-byte stores per lane, issued during the NEXT group's MFMA loop, one every other
+// k-step, so the write stream runs under the matrix work instead of in a burst between stages (every
+// workgroup reaches its epilogue at about the same time).  Stage barriers wait with an exact vmcnt for
+// the weight loads issued before those stores.
 constexpr int kQkvWaves = 8;
 constexpr int kQkvTps = 4;
 constexpr int kQkvStages = (kQkvgTiles + kQkvTps - 1) / kQkvTps;
+constexpr int kQkvGroupStores = 8;  // 2 tiles x 4 register groups
 
 __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
                                                   const float* __restrict__ bgate, const float* __restrict__ rope,
@@ -196,7 +203,30 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
         rsn[half][g] = *reinterpret_cast<const float2*>(sr + 16 * half + 4 * g + 2 * hh);
       }
   }
-  const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
+
+  // q/k rows are chunk-major: features 8c..8c+7 of position p at ((s*8 + h)*8 + c)*Lpad + p, so the 32
+  // lanes of a half-wave store 32 consecutive 16-byte chunks (hh fills bytes 8hh..8hh+7).
+  const int64_t qk_off = (int64_t(s) * kHeads * 8 * Lpad + p) * 8 + 4 * hh;
+  // V^T rows: lane 4q + r of a half-wave stores row r of its register group at positions 4q..4q+3
+  const int qd = lane & 3;
+  const int64_t v_off = (int64_t(s) * kHeads * kHeadDim + 4 * hh + qd) * Lpad + (p & ~3);
+  u32x2 pend[kQkvGroupStores];  // the previous group's packed outputs
+
+  // Store i of the outputs of group grp of stage ps: tile 4ps + 2grp + i/4, register group i%4.  Every
+  // offset beyond the lane's own is wave-uniform.
+  auto store_pending = [&](int ps, int grp, int i) __attribute__((always_inline)) {
+    const int tt = 2 * grp + (i >> 2), g = i & 3, t = kQkvTps * ps + tt, half = tt & 1;
+    if (ps < 8) {
+      const int h = (t & 15) >> 1;
+      uint16_t* base = (ps < 4 ? Q : K) + qk_off;
+      const int64_t off = int64_t(__builtin_amdgcn_readfirstlane((h * 8 + 4 * half + g) * Lpad)) * 8;
+      *reinterpret_cast<u32x2*>(base + off) = pend[i];
+    } else {
+      const int h = (t - 32) >> 1;
+      const int drow = h * kHeadDim + 32 * half + 8 * g;  // row of V^T, less 4hh + r
+      *reinterpret_cast<u32x2*>(Vt + v_off + int64_t(__builtin_amdgcn_readfirstlane(drow * Lpad))) = pend[i];
+    }
+  };
 
   auto issue = [&](int stage, int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -207,16 +237,31 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
     }
   };
   issue(0, 0);
+  // Everything loaded so far has landed (the first stage barrier waits for it anyway): stated as the
+  // builtin so that the compiler's own waitcnt insertion, which cannot tell the barrier branches below
+  // apart, adds no waits for the xn and rotary registers inside the loop.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
   for (int stage = 0; stage < kQkvStages; ++stage) {
-    stage_barrier();
+    // This stage's weight loads were issued at the top of the previous stage, whose two loops then
+    // issued 8 stores each (only the second loop at stage 0).
+    if (active && stage >= 2)
+      vmcnt_barrier<2 * kQkvGroupStores>();
+    else if (active && stage == 1)
+      vmcnt_barrier<kQkvGroupStores>();
+    else
+      vmcnt_barrier<0>();
     if (stage + 1 < kQkvStages) issue(stage + 1, (stage + 1) & 1);
     if (!active) continue;
     const u32x4* Ls = lds[stage & 1];
     if (stage == kQkvStages - 1) {  // the gate tile: rows 0..7 live in register group 0 of both half-waves
       f32x16 acc = zero16();
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) acc = mfma32(Ls[ks * 64 + lane], bx[ks], acc);
+      for (int ks = 0; ks < 16; ++ks) {
+        acc = mfma32(Ls[ks * 64 + lane], bx[ks], acc);
+        if (ks & 1) store_pending(stage - 1, 1, ks >> 1);
+      }
       if (valid) {
+        const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
         f32x4 gv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) gv[r] = 1.0f / (1.0f + expf(-(acc[r] + bg[r])));
@@ -224,62 +269,70 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
       }
       continue;
     }
-    f32x16 acc[kQkvTps];
-    u32x4 a[kQkvTps];
 #pragma unroll
-    for (int tt = 0; tt < kQkvTps; ++tt) {
-      acc[tt] = zero16();
-      a[tt] = Ls[tt * 16 * 64 + lane];
-    }
+    for (int grp = 0; grp < 2; ++grp) {
+      f32x16 acc[2];
+      u32x4 a[2];
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {  // operands of k-step ks+1 are read while ks multiplies
-      u32x4 an[kQkvTps];
-#pragma unroll
-      for (int tt = 0; tt < kQkvTps; ++tt)
-        if (ks + 1 < 16) an[tt] = Ls[(tt * 16 + ks + 1) * 64 + lane];
-#pragma unroll
-      for (int tt = 0; tt < kQkvTps; ++tt) acc[tt] = mfma32(a[tt], bx[ks], acc[tt]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int tt = 0; tt < kQkvTps; ++tt)
-        if (ks + 1 < 16) a[tt] = an[tt];
-    }
-    if (stage < 8) {  // q (stages 0-3) or k (4-7): rotate interleaved pairs in fp32, store bf16 rows
-      // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
-      const float sc = stage < 4 ? kLog2e : 1.0f;
-      uint16_t* base = stage < 4 ? Q : K;
-#pragma unroll
-      for (int tt = 0; tt < kQkvTps; ++tt) {
-        const int t = kQkvTps * stage + tt, h = (t & 15) >> 1, half = tt & 1;
-        // chunk-major rows: features 8c..8c+7 of position p at ((s*8 + h)*8 + c)*Lpad + p, so the
-        // 32 lanes of a half-wave store 32 consecutive 16-byte chunks (hh fills bytes 8hh..8hh+7)
-        uint16_t* dst = base + ((int64_t(s) * kHeads + h) * 8 * Lpad + p) * 8 + 4 * hh;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int c8 = __builtin_amdgcn_readfirstlane((4 * half + g) * Lpad * 8);  // chunk 4 half + g
-          const float2 c = rc[half][g], sn = rsn[half][g];
-          const float a0 = acc[tt][4 * g], a1 = acc[tt][4 * g + 1], a2 = acc[tt][4 * g + 2], a3 = acc[tt][4 * g + 3];
-          u32x2 o = {0u, 0u};
-          if (valid) {
-            o[0] = pk_bf16(fmaf(a0, c.x, -(a1 * sn.x)) * sc, fmaf(a1, c.x, a0 * sn.x) * sc);
-            o[1] = pk_bf16(fmaf(a2, c.y, -(a3 * sn.y)) * sc, fmaf(a3, c.y, a2 * sn.y) * sc);
-          }
-          *reinterpret_cast<u32x2*>(dst + c8) = o;
-        }
+      for (int u = 0; u < 2; ++u) {
+        acc[u] = zero16();
+        a[u] = Ls[(2 * grp + u) * 16 * 64 + lane];
       }
-    } else {  // v: transposed store, 32 lanes write 32 consecutive positions of one row
-      // per-lane base (sequence, half-wave rows, position); every row offset below is wave-uniform
-      uint16_t* vb = Vt + int64_t(s) * kHeads * kHeadDim * Lpad + int64_t(4 * hh) * Lpad + p;
+      const bool pending = grp == 1 || stage > 0;
 #pragma unroll
-      for (int tt = 0; tt < kQkvTps; ++tt) {
-        const int t = kQkvTps * stage + tt, h = (t - 32) >> 1, half = tt & 1;
+      for (int ks = 0; ks < 16; ++ks) {  // operands of k-step ks+1 are read while ks multiplies
+        u32x4 an[2];
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+        for (int u = 0; u < 2; ++u)
+          if (ks + 1 < 16) an[u] = Ls[((2 * grp + u) * 16 + ks + 1) * 64 + lane];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int drow = h * kHeadDim + 32 * half + 8 * g + r;  // row of V^T, less 4hh
-            vb[int64_t(__builtin_amdgcn_readfirstlane(drow * Lpad))] =
-                valid ? to_bf16(acc[tt][4 * g + r]) : uint16_t(0);
+        for (int u = 0; u < 2; ++u) acc[u] = mfma32(a[u], bx[ks], acc[u]);
+        if ((ks & 1) && pending) store_pending(grp ? stage : stage - 1, grp ^ 1, ks >> 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (ks + 1 < 16) a[u] = an[u];
+      }
+      if (stage < 8) {  // q (stages 0-3) or k (4-7): rotate interleaved pairs in fp32, pack bf16 rows
+        // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
+        const float sc = stage < 4 ? kLog2e : 1.0f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int half = u;  // tiles 2grp and 2grp+1 are halves 0 and 1 of one head
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float2 c = rc[half][g], sn = rsn[half][g];
+            const float a0 = acc[u][4 * g], a1 = acc[u][4 * g + 1], a2 = acc[u][4 * g + 2], a3 = acc[u][4 * g + 3];
+            u32x2 o = {0u, 0u};
+            if (valid) {
+              o[0] = pk_bf16(fmaf(a0, c.x, -(a1 * sn.x)) * sc, fmaf(a1, c.x, a0 * sn.x) * sc);
+              o[1] = pk_bf16(fmaf(a2, c.y, -(a3 * sn.y)) * sc, fmaf(a3, c.y, a2 * sn.y) * sc);
+            }
+            pend[4 * u + g] = o;
+          }
+        }
+      } else {  // v: register group g holds rows 8g + 4hh + r (r = 0..3) of position p; a 4 x 4
+        // transpose across each lane quad (two DPP exchanges) leaves lane 4q + r with row r of
+        // positions 4q..4q+3, so a half-wave's store covers 4 rows x 64 contiguous bytes.
+        const bool b1 = qd & 2, b0 = qd & 1;
+        // byte selectors of v_perm_b32 (bytes 0-3 from the second operand, 4-7 from the first)
+        const uint32_t sel_send = b0 ? 0x05040100u : 0x07060302u;
+        const uint32_t sel_f0 = b0 ? 0x03020504u : 0x05040100u;
+        const uint32_t sel_f1 = b0 ? 0x03020706u : 0x07060100u;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            // d0/d1: rows (0,1)/(2,3) of this position (zero past the sequence end)
+            const uint32_t d0 = valid ? pk_bf16(acc[u][4 * g], acc[u][4 * g + 1]) : 0u;
+            const uint32_t d1 = valid ? pk_bf16(acc[u][4 * g + 2], acc[u][4 * g + 3]) : 0u;
+            // exchange with lane ^ 2: lanes 0,1 keep rows 0,1 of positions q, q+2; lanes 2,3 rows 2,3
+            const uint32_t r1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(b1 ? d0 : d1), 0x4E, 0xF, 0xF, true));
+            const uint32_t e0 = b1 ? r1 : d0, e1 = b1 ? d1 : r1;
+            // exchange halves with lane ^ 1: lane r ends with row r of positions 0..3
+            const uint32_t snd = __builtin_amdgcn_perm(e1, e0, sel_send);
+            const uint32_t r2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(snd), 0xB1, 0xF, 0xF, true));
+            pend[4 * u + g] = u32x2{__builtin_amdgcn_perm(r2, e0, sel_f0), __builtin_amdgcn_perm(r2, e1, sel_f1)};
           }
       }
     }
@@ -509,18 +562,6 @@ __device__ __forceinline__ void attn_tile(const u32x4* __restrict__ Kl, const u3
 // 2 for a K tile, 4 for K + V), and the barrier makes every wave's share visible.
 constexpr int kAttBufs = 3;
 
-// The wait is explicit, so the barrier is the bare s_barrier: __syncthreads' release fence would also
-// wait for the younger tiles' LDS-DMA loads.  The empty asm with a memory clobber keeps the compiler
-// from moving LDS accesses across the barrier.
-template <int N>
-__device__ __forceinline__ void tile_barrier() {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);  // vmcnt(N) expcnt(7) lgkmcnt(15)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ Vt, const float* __restrict__ G,
                                                    uint16_t* __restrict__ O, int mode, int L, int Lpad, int T,
@@ -566,7 +607,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
         stage_k_tile(Kh, i, Lpad, lds[i][0], wave, lane);
         stage_v_tile(Vh, i, Lpad, lds[i][1], wave, lane);
       }
-    tile_barrier<4 * (kAttBufs - 2)>();  // tile 0 (nkt >= 2 >= kAttBufs - 1)
+    vmcnt_barrier<4 * (kAttBufs - 2)>();  // tile 0 (nkt >= 2 >= kAttBufs - 1)
     if (kAttBufs - 1 < nkt) {
       stage_k_tile(Kh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][0], wave, lane);
       stage_v_tile(Vh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][1], wave, lane);
@@ -574,9 +615,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
     if (active) attn_tile<true, false, SAFE>(lds[0][0], lds[0][1], qb, 0, L, j, hh, negc, lsum, o);
     for (int kt = 1; kt < nkt - 1; ++kt) {
       if (kt + kAttBufs - 2 < nkt)  // K and V: 4 loads per younger tile in flight
-        tile_barrier<4 * (kAttBufs - 2)>();
+        vmcnt_barrier<4 * (kAttBufs - 2)>();
       else
-        tile_barrier<0>();
+        vmcnt_barrier<0>();
       if (kt + kAttBufs - 1 < nkt) {
         const int b = (kt + kAttBufs - 1) % kAttBufs;
         stage_k_tile(Kh, kt + kAttBufs - 1, Lpad, lds[b][0], wave, lane);
@@ -585,7 +626,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
       if (active)
         attn_tile<false, false, SAFE>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negc, lsum, o);
     }
-    tile_barrier<0>();
+    vmcnt_barrier<0>();
     if (active)
       attn_tile<false, true, SAFE>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L,
                                    j, hh, negc, lsum, o);

@@ -75,16 +75,6 @@ __device__ __forceinline__ void fs_issue_b(int h, u32x4* buf, const u32x4* wq, i
   }
 }
 
-// vmcnt(N): this thread's vector memory operations are complete except the N most recent (they complete
-// in issue order), then all waves meet.  The LDS-DMA loads of a stage count among them.
-template <int N>
-__device__ __forceinline__ void fs_barrier() {
-  static_assert(N >= 0 && N < 16 * 4, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Key (or token) of register R of half-wave hh in a 32-row accumulator tile: row 8(R/4) + 4hh + R%4.
 __device__ __forceinline__ int acc_row(int R, int hh) { return 8 * (R >> 2) + 4 * hh + (R & 3); }
 
@@ -194,7 +184,7 @@ __global__ __launch_bounds__(256, 1) void k_qkv_attn_short(const uint16_t* __res
     qoff[qt] = q < L ? q * tok_stride * (kHeads * kHeadDim * 2) : kFsDropped;
   }
   __syncthreads();  // the rotary table
-  fs_barrier<0>();  // the gate tile and stage A of head 0
+  vmcnt_barrier<0>();  // the gate tile and stage A of head 0
   fs_issue_b(0, Lb, wq, wave, lane);
   float gv[2][4];  // sigmoid gates of heads 4hh + r for the tokens of column tile t
   if (active) {
@@ -256,9 +246,9 @@ __global__ __launch_bounds__(256, 1) void k_qkv_attn_short(const uint16_t* __res
     }
     // stage B of head h has landed (its loads are older than the 16 stores issued above)
     if (active)
-      fs_barrier<kFsStoresPerHead>();
+      vmcnt_barrier<kFsStoresPerHead>();
     else
-      fs_barrier<0>();
+      vmcnt_barrier<0>();
     if (h + 1 < kHeads) fs_issue_a(h + 1, La, wq, wave, lane);
     if (active) {
       // ---- stage B: v (swapped product, tokens on the rows) with the softmax of S^T between its MFMAs
@@ -356,7 +346,7 @@ __global__ __launch_bounds__(256, 1) void k_qkv_attn_short(const uint16_t* __res
       }
     }
     // stage A of head h + 1 has landed (the stores of head h - 1 went out during stage A of head h)
-    fs_barrier<0>();
+    vmcnt_barrier<0>();
     if (h + 1 < kHeads) fs_issue_b(h + 1, Lb, wq, wave, lane);
   }
   if (active) {
