@@ -5,21 +5,25 @@
 // bf16 rounding, bf16 q, k, v and unnormalised P, the exact row max over the valid keys, an fp32 sum of
 // e = 2^(s - m), and O = (P.V) * gate / sum rounded to bf16 in token order.
 //
-// One wave owns one sequence.  Its (up to) 64 positions are two 32-token column tiles whose xn rows stay
-// in registers (bf16, natural k order).  The 49 weight tiles of W_qkvg stream through LDS, shared by the
-// 4 waves (sequences) of a workgroup: the gate tile once, then per head two stages, A (the q and k tiles,
-// 64 KB) and B (the v tiles, 32 KB), each in its own LDS buffer so that one loads while the other is read.
-// Every operand block read from LDS feeds two MFMAs (the two column tiles).
+// A sequence is two 32-position halves, one wave each, and the two waves of a sequence share a SIMD, so
+// each SIMD runs two waves and one wave's rotary, softmax and packing work can run under the other's
+// MFMAs.  A wave keeps its 32 positions' xn rows in registers (bf16, natural k order) and computes q, k
+// and v of its own positions; each half writes its K and V^T operand blocks to LDS and reads the other
+// half's, so that every wave attends its 32 queries over all 64 keys.  A workgroup is 4 sequences (8
+// waves).  The 49 weight tiles of W_qkvg stream through a 2-deep LDS ring of 32 KB stages: the gate tile,
+// then per head the q tiles, the k tiles and the v tiles.
 //
-// Schedule (one wave per SIMD, so VALU work hides only under the same wave's MFMAs): stage A runs the q, k
-// products of head half 0, then those of half 1 with the rotary of half 0 and the scaling and stores of
-// the previous head's output spread between them, then S^T; stage B runs the v products with the
-// softmax of S^T spread between them, then P.V.  O is written with bounds-checked buffer stores (lanes
-// past the sequence use an out-of-range offset), always 16 per wave and head, so the barrier before the
-// next stage B waits for that stage's loads with an exact vmcnt and never for the stores.
+// Per head h (stages Aq, Ak, B):
+//   Aq: P.V of head h - 1 (its V^T now visible from both halves) and its 8 bounds-checked O stores,
+//       spread between the q products of head h;
+//   Ak: the k products, with the rotary of q between them; then the rotary of k, written to LDS;
+//   B:  S^T = K.Q^T over both halves' keys, then the v products with the softmax of S^T between them;
+//       then V^T packed and written to LDS.
+// The stage barriers wait for the stage's loads with an exact vmcnt (the 8 O stores of a head are
+// issued after the loads of the following stage and are never waited for) and for the LDS exchange.
 //
 // No data crosses lanes between the projection and the attention:
-//   * q and k come out of C = W . xn^T with lane (j, hh) holding token j of a column tile and features
+//   * q and k come out of C = W . xn^T with lane (j, hh) holding token j of the column tile and features
 //     8g + 4hh + r.  Packed to bf16 in that "register order", q is the B operand (Q^T) and k the A
 //     operand (K) of S^T = K . Q^T: both use the same permutation of the 16 head features of a k-step,
 //     which leaves the dot products unchanged.
@@ -32,335 +36,394 @@
 
 namespace trf {
 
-constexpr int kFsWaves = 4;              // sequences per workgroup, one wave (and SIMD) each
-constexpr int kFsBlocksA = 64;           // q and k tiles of one head: 2 kinds x 2 halves x 16 k-steps of 1 KB
-constexpr int kFsBlocksB = 32;           // v tiles of one head: 2 halves x 16 k-steps
-constexpr int kFsBlocksG = 16;           // the gate tile
-constexpr int kFsRopePairs = 16;         // pairs of rotary pairs per position (32 pairs)
-constexpr int kFsRopeVecs = 2 * kFsRopePairs * 64;  // float2 [cos, sin][pair pair][position]
-constexpr int kFsStoresPerHead = 16;     // O stores per wave and head: 2 query tiles x 2 feature tiles x 4
-// LDS layout, in 16-byte units: stage A, stage B, the gate tile, the rotary table (128 KB).
-constexpr int kFsOffB = kFsBlocksA * 64;
-constexpr int kFsOffG = kFsOffB + kFsBlocksB * 64;
-constexpr int kFsOffRope = kFsOffG + kFsBlocksG * 64;
-constexpr int kFsLdsVecs = kFsOffRope + kFsRopeVecs / 2;
-constexpr int kFsDropped = 0x40000000;   // buffer offset past any sequence's output: the store is dropped
+constexpr int kFsSeqs = 4;                       // sequences per workgroup
+constexpr int kFsWaves = 2 * kFsSeqs;            // one wave per 32-position half; waves w, w + 4 share a SIMD
+constexpr int kFsStageBlocks = 32;               // 1 KB operand blocks per weight stage
+constexpr int kFsStages = 1 + 3 * kHeads;        // the gate tile, then q, k and v tiles per head
+constexpr int kFsStoresPerHead = 8;              // O stores per wave and head: 2 feature tiles x 4 groups
+// LDS layout, in 16-byte units: the two weight stages, then the K and V^T operand blocks exchanged
+// between the halves, [sequence][half][k-step][lane] (128 KB).
+constexpr int kFsOffKx = 2 * kFsStageBlocks * 64;
+constexpr int kFsOffVx = kFsOffKx + kFsSeqs * 2 * 4 * 64;
+constexpr int kFsLdsVecs = kFsOffVx + kFsSeqs * 2 * 4 * 64;
+constexpr int kFsDropped = 0x40000000;  // buffer offset past any sequence's output: the store is dropped
 
-// This wave's share of the gate tile (the last tile of W_qkvg).
-__device__ __forceinline__ void fs_issue_gate(u32x4* buf, const u32x4* wq, int wave, int lane) {
+// This wave's share of stage n into LDS buffer buf: the gate tile (n = 0: k-step b of the last tile), or
+// for n = 1 + 3h + kind (kind 0 q, 1 k, 2 v) block 16c + ks = k-step ks of tile 16 kind + 2h + c.
+__device__ __forceinline__ void fs_issue(int n, u32x4* buf, const u32x4* wq, int wave, int lane) {
+  if (n >= kFsStages) return;
+  if (n == 0) {
 #pragma unroll
-  for (int i = 0; i < kFsBlocksG / kFsWaves; ++i) {
-    const int b = (kFsBlocksG / kFsWaves) * wave + i;
-    lds_load_block(wq + (int64_t(kQkvgTiles - 1) * 16 + b) * 64, buf + b * 64, lane);
+    for (int i = 0; i < 2; ++i) {
+      const int b = 2 * wave + i;
+      lds_load_block(wq + (int64_t(kQkvgTiles - 1) * 16 + b) * 64, buf + b * 64, lane);
+    }
+    return;
   }
-}
-
-// Stage A of head h: block 32 kind + 16 c + ks is k-step ks of tile 16 kind + 2h + c (kind 0 q, 1 k).
-__device__ __forceinline__ void fs_issue_a(int h, u32x4* buf, const u32x4* wq, int wave, int lane) {
+  const int h = (n - 1) / 3, kind = (n - 1) % 3;
 #pragma unroll
-  for (int i = 0; i < kFsBlocksA / kFsWaves; ++i) {
-    const int b = (kFsBlocksA / kFsWaves) * wave + i;
-    const int t = 16 * (b >> 5) + 2 * h + ((b >> 4) & 1);
+  for (int i = 0; i < kFsStageBlocks / kFsWaves; ++i) {
+    const int b = (kFsStageBlocks / kFsWaves) * wave + i;
+    const int t = 16 * kind + 2 * h + (b >> 4);
     lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, buf + b * 64, lane);
   }
 }
 
-// Stage B of head h: block 16 c + ks is k-step ks of v tile 32 + 2h + c.
-__device__ __forceinline__ void fs_issue_b(int h, u32x4* buf, const u32x4* wq, int wave, int lane) {
-#pragma unroll
-  for (int i = 0; i < kFsBlocksB / kFsWaves; ++i) {
-    const int b = (kFsBlocksB / kFsWaves) * wave + i;
-    const int t = 32 + 2 * h + (b >> 4);
-    lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, buf + b * 64, lane);
-  }
+// This thread's vector memory operations have completed except the N most recent, its LDS operations
+// have all completed (the K / V^T exchange), then all waves meet.
+template <int N>
+__device__ __forceinline__ void fs_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);  // vmcnt(N) expcnt(7) lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Key (or token) of register R of half-wave hh in a 32-row accumulator tile: row 8(R/4) + 4hh + R%4.
 __device__ __forceinline__ int acc_row(int R, int hh) { return 8 * (R >> 2) + 4 * hh + (R & 3); }
 
-// q and k products of head half c (4 accumulator chains over 16 k-steps; operands read one k-step ahead);
-// after(ks) runs after the MFMAs of k-step ks.
-template <class After>
-__device__ __forceinline__ void fs_qk_half(const u32x4* __restrict__ La, int c, const u32x4 (&bx)[2][16], int lane,
-                                           f32x16 (&qa)[2], f32x16 (&ka)[2], After after) {
-#pragma unroll
-  for (int t = 0; t < 2; ++t) qa[t] = ka[t] = zero16();
-  u32x4 aq = La[(16 * c) * 64 + lane], ak = La[(32 + 16 * c) * 64 + lane];
-#pragma unroll
-  for (int ks = 0; ks < 16; ++ks) {
-    u32x4 nq, nk;
-    if (ks + 1 < 16) {
-      nq = La[(16 * c + ks + 1) * 64 + lane];
-      nk = La[(32 + 16 * c + ks + 1) * 64 + lane];
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) qa[t] = mfma32(aq, bx[t][ks], qa[t]);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) ka[t] = mfma32(ak, bx[t][ks], ka[t]);
-    after(ks);
-    __builtin_amdgcn_sched_barrier(0);
-    if (ks + 1 < 16) {
-      aq = nq;
-      ak = nk;
-    }
-  }
-}
-
-// Rotary of register group g (rows 8g + 4hh + r) of column tile t of head half c, fp32 (q times log2 e),
-// into the bf16 operands: q as the B operand Q^T, k as the A operand K, k-step g / 2 of the half.
-__device__ __forceinline__ void fs_rotate(const f32x16& qa, const f32x16& ka, const float2* __restrict__ ropeL, int c,
-                                          int t, int g, int j, int hh, u32x4& qb, u32x4& kb) {
-  const int p = 32 * t + j, pp = 8 * c + 2 * g + hh;  // pairs 2pp, 2pp + 1 = 16c + 4g + 2hh + {0, 1}
-  const float2 cs = ropeL[pp * 64 + p], sn = ropeL[(kFsRopePairs + pp) * 64 + p];
-  const float q0 = qa[4 * g], q1 = qa[4 * g + 1], q2 = qa[4 * g + 2], q3 = qa[4 * g + 3];
-  qb[2 * (g & 1)] = pk_bf16(fmaf(q0, cs.x, -(q1 * sn.x)) * kLog2e, fmaf(q1, cs.x, q0 * sn.x) * kLog2e);
-  qb[2 * (g & 1) + 1] = pk_bf16(fmaf(q2, cs.y, -(q3 * sn.y)) * kLog2e, fmaf(q3, cs.y, q2 * sn.y) * kLog2e);
-  const float k0 = ka[4 * g], k1 = ka[4 * g + 1], k2 = ka[4 * g + 2], k3 = ka[4 * g + 3];
-  kb[2 * (g & 1)] = pk_bf16(fmaf(k0, cs.x, -(k1 * sn.x)), fmaf(k1, cs.x, k0 * sn.x));
-  kb[2 * (g & 1) + 1] = pk_bf16(fmaf(k2, cs.y, -(k3 * sn.y)), fmaf(k3, cs.y, k2 * sn.y));
-}
-
-// The output of one head waiting to be scaled and stored: O^T accumulators [d tile][query tile], the
-// per-query scale gate / sum, and the byte offset of each query tile's row (kFsDropped past the end).
-struct FsPending {
-  f32x16 o[2][2];
-  float sc[2];
-  int off[2];
+// The rotary cos/sin of this lane's position: pairs 16c + 4g + 2hh + {0, 1}, the ones that register
+// group g (rows 8g + 4hh + r) of head half c rotates.
+struct FsRope {
+  float2 cs[2][4], sn[2][4];
 };
 
-// Unit u (0..15) of storing a pending head: query tile u / 8, feature tile (u / 4) % 2, group u % 4.
-__device__ __forceinline__ void fs_store_unit(const FsPending& pd, int u, int h, int hh, __amdgpu_buffer_rsrc_t ores) {
-  const int qt = u >> 3, dt = (u >> 2) & 1, g = u & 3;
-  const float sc = pd.sc[qt];
-  const f32x16& o = pd.o[dt][qt];
-  const u32x2 v = {pk_bf16(o[4 * g] * sc, o[4 * g + 1] * sc), pk_bf16(o[4 * g + 2] * sc, o[4 * g + 3] * sc)};
-  const int off = pd.off[qt] + 2 * (h * kHeadDim + 32 * dt + row_of_group(g, hh));
+// Rotary of register group g of head half c, fp32, scaled, into the bf16 operand of k-step 2c + g/2
+// (elements 2(g%2), 2(g%2) + 1).
+__device__ __forceinline__ void fs_rotate(const f32x16& a, const FsRope& rp, int c, int g, float scale, u32x4& out) {
+  const float2 cs = rp.cs[c][g], sn = rp.sn[c][g];
+  const float a0 = a[4 * g], a1 = a[4 * g + 1], a2 = a[4 * g + 2], a3 = a[4 * g + 3];
+  out[2 * (g & 1)] = pk_bf16(fmaf(a0, cs.x, -(a1 * sn.x)) * scale, fmaf(a1, cs.x, a0 * sn.x) * scale);
+  out[2 * (g & 1) + 1] = pk_bf16(fmaf(a2, cs.y, -(a3 * sn.y)) * scale, fmaf(a3, cs.y, a2 * sn.y) * scale);
+}
+
+// One head's output of this wave's 32 queries, from P.V to the store: O^T accumulators [feature tile],
+// the per-query scale gate / sum and the query row's byte offset (kFsDropped past the sequence end).
+struct FsOut {
+  f32x16 o[2];
+  float sc;
+  int off;
+};
+
+// Store unit u (0..7) of a head's output: feature tile u / 4, register group u % 4.
+__device__ __forceinline__ void fs_store_unit(const FsOut& po, int u, int h, int hh, __amdgpu_buffer_rsrc_t ores) {
+  const int dt = u >> 2, g = u & 3;
+  const f32x16& o = po.o[dt];
+  const u32x2 v = {pk_bf16(o[4 * g] * po.sc, o[4 * g + 1] * po.sc), pk_bf16(o[4 * g + 2] * po.sc, o[4 * g + 3] * po.sc)};
+  const int off = po.off + 2 * (h * kHeadDim + 32 * dt + row_of_group(g, hh));
   __builtin_amdgcn_raw_buffer_store_b64(v, ores, off, 0, 0);
 }
 
-__global__ __launch_bounds__(256, 1) void k_qkv_attn_short(const uint16_t* __restrict__ xn,
-                                                          const u32x4* __restrict__ wq,
-                                                          const float* __restrict__ bgate,
-                                                          const float* __restrict__ rope, int mode, int nseq,
-                                                          int L, int T, int F, uint16_t* __restrict__ O) {
-  __shared__ u32x4 smem[kFsLdsVecs];  // one LDS object: stage A, stage B, gate tile, rotary table
-  u32x4* La = smem;
-  u32x4* Lb = smem + kFsOffB;
-  u32x4* Lg = smem + kFsOffG;
-  float2* ropeL = reinterpret_cast<float2*>(smem + kFsOffRope);
-  const int lane = threadIdx.x & 63, wave = wave_id();
-  const int j = lane & 31, hh = lane >> 5;
-  const int s = blockIdx.x * kFsWaves + wave;
-  const bool active = s < nseq;  // idle waves still stage weights and meet every barrier
+// What one head leaves for the next stage Aq: this half's V^T operands [feature tile][key k-step], the
+// P^T operands of its queries [key k-step 2 kt + kk], and the scale and offset of its output.
+struct FsCarry {
+  u32x4 vb[2][2];
+  u32x4 pb[4];
+  float sc;
+  int off;
+};
 
-  fs_issue_gate(Lg, wq, wave, lane);
-  fs_issue_a(0, La, wq, wave, lane);
-  // rotary table [2][L][32] fp32 -> LDS float2 [cos, sin][pair pair][position] (zero past L), so that the
-  // 32 lanes of a half-wave read 32 consecutive positions of one pair pair
-  for (int i = threadIdx.x; i < kFsRopeVecs; i += 64 * kFsWaves) {
-    const int cs = i >> 10, pp = (i >> 6) & 15, p = i & 63;
-    float2 v = {0.f, 0.f};
-    if (p < L) v = *reinterpret_cast<const float2*>(rope + (int64_t(cs) * L + p) * 32 + 2 * pp);
-    ropeL[i] = v;
-  }
-  u32x4 bx[2][16];  // xn of positions 32t + j (zero past L), natural k order
+// P.V of a head: the other half's V^T operands come from LDS.
+__device__ __forceinline__ void fs_pv(const FsCarry& cy, const u32x4* __restrict__ vx_other, int th, int lane,
+                                      FsOut& po) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int p = 32 * t + j;
-    const bool valid = active && p < L;
-    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? token_of(mode, s, p, T, F) : 0) * kDim);
+  for (int dt = 0; dt < 2; ++dt) {
+    po.o[dt] = zero16();
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) bx[t][ks] = valid ? xr[2 * ks + hh] : zero4();
-  }
-  // O of this sequence as a buffer: token of position p at byte (token_of(p) - token_of(0)) * 1 KB
-  const int64_t tok0 = active ? token_of(mode, s, 0, T, F) : 0;
-  const int tok_stride = mode == 0 ? F : 1;
-  const __amdgpu_buffer_rsrc_t ores =
-      buffer_rsrc(O + tok0 * (kHeads * kHeadDim), active ? ((L - 1) * tok_stride + 1) * kHeads * kHeadDim * 2 : 0);
-  int qoff[2];
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int q = 32 * qt + j;
-    qoff[qt] = q < L ? q * tok_stride * (kHeads * kHeadDim * 2) : kFsDropped;
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 v = kt == th ? cy.vb[dt][kk] : vx_other[(2 * dt + kk) * 64 + lane];
+        po.o[dt] = mfma32(v, cy.pb[2 * kt + kk], po.o[dt]);
+      }
   }
-  __syncthreads();  // the rotary table
-  vmcnt_barrier<0>();  // the gate tile and stage A of head 0
-  fs_issue_b(0, Lb, wq, wave, lane);
-  float gv[2][4];  // sigmoid gates of heads 4hh + r for the tokens of column tile t
-  if (active) {
-    f32x16 ga[2] = {zero16(), zero16()};
+  po.sc = cy.sc;
+  po.off = cy.off;
+}
+
+struct FsCtx {
+  const u32x4* wq;
+  FsRope rope;
+  const u32x4* kx_other;
+  u32x4* kx_own;
+  const u32x4* vx_other;
+  u32x4* vx_own;
+  __amdgpu_buffer_rsrc_t ores;
+  int qoff, L, p, th, hh, lane, wave;
+  bool active;
+  float gv[4];  // sigmoid gates of heads 4hh + r for this lane's query
+};
+
+// One head: stages Aq (LDS buffer PA), Ak (1 - PA) and B (PA) of stage numbers n, n + 1, n + 2, n = 1 + 3h.
+// The buffer parity is a template argument so that every LDS address is a compile-time constant plus a
+// lane term: the compiler can then tell the operand reads from the direct-to-LDS loads into the other
+// buffer and does not wait for those loads.
+template <int PA>
+__device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, const u32x4 (&bx)[16], FsCarry& cy) {
+  u32x4* const La = smem + PA * kFsStageBlocks * 64;
+  u32x4* const Lk = smem + (1 - PA) * kFsStageBlocks * 64;
+  const int n = 1 + 3 * h, lane = cx.lane;
+
+  // ---- stage Aq: P.V and stores of head h - 1, q products of head h
+  fs_barrier<0>();  // q tiles landed; V^T of head h - 1 written by both halves
+  fs_issue(n + 1, Lk, cx.wq, cx.wave, lane);
+  f32x16 qa[2];
+  if (cx.active) {
+    FsOut po;
+    fs_pv(cy, cx.vx_other, cx.th, lane, po);  // for h = 0 a dummy whose stores are all dropped
+#pragma unroll
+    for (int c = 0; c < 2; ++c) qa[c] = zero16();
+    u32x4 a0 = La[lane], a1 = La[16 * 64 + lane];
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) {
-      const u32x4 a = Lg[ks * 64 + lane];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) ga[t] = mfma32(a, bx[t][ks], ga[t]);
+      u32x4 n0, n1;
+      if (ks + 1 < 16) {
+        n0 = La[(ks + 1) * 64 + lane];
+        n1 = La[(16 + ks + 1) * 64 + lane];
+      }
+      qa[0] = mfma32(a0, bx[ks], qa[0]);
+      qa[1] = mfma32(a1, bx[ks], qa[1]);
+      if (ks & 1) fs_store_unit(po, ks >> 1, h - 1, cx.hh, cx.ores);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < 16) {
+        a0 = n0;
+        a1 = n1;
+      }
     }
-    const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) gv[t][r] = 1.0f / (1.0f + expf(-(ga[t][r] + bg[r])));
   }
 
-  // The previous head's output, stored during the next head's stage A.  Before head 0 it is a dummy
-  // whose stores are all dropped, so that every head issues the same 16 stores.
-  FsPending pd;
+  // ---- stage Ak: k products with the rotary of q between them, then the rotary of k into LDS
+  if (cx.active)
+    fs_barrier<kFsStoresPerHead>();  // k tiles landed (the 8 stores above are younger)
+  else
+    fs_barrier<0>();
+  fs_issue(n + 2, La, cx.wq, cx.wave, lane);
+  u32x4 qb[2][2], kb[2][2];  // [head half][k-step of the half]
+  if (cx.active) {
+    f32x16 ka[2];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    pd.o[0][qt] = pd.o[1][qt] = zero16();
-    pd.sc[qt] = 0.f;
-    pd.off[qt] = kFsDropped;
+    for (int c = 0; c < 2; ++c) ka[c] = zero16();
+    u32x4 a0 = Lk[lane], a1 = Lk[16 * 64 + lane];
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      u32x4 n0, n1;
+      if (ks + 1 < 16) {
+        n0 = Lk[(ks + 1) * 64 + lane];
+        n1 = Lk[(16 + ks + 1) * 64 + lane];
+      }
+      ka[0] = mfma32(a0, bx[ks], ka[0]);
+      ka[1] = mfma32(a1, bx[ks], ka[1]);
+      if (ks & 1) {
+        const int u = ks >> 1, c = u >> 2, g = u & 3;
+        fs_rotate(qa[c], cx.rope, c, g, kLog2e, qb[c][g >> 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < 16) {
+        a0 = n0;
+        a1 = n1;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) fs_rotate(ka[u >> 2], cx.rope, u >> 2, u & 3, 1.0f, kb[u >> 2][(u & 3) >> 1]);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) cx.kx_own[(2 * c + kk) * 64 + lane] = kb[c][kk];
+  }
+
+  // ---- stage B: S^T over both halves' keys, v products with the softmax between them, V^T into LDS
+  fs_barrier<0>();  // v tiles landed; K written by both halves
+  fs_issue(n + 3, Lk, cx.wq, cx.wave, lane);
+  if (cx.active) {
+    f32x16 sacc[2];  // [key tile]
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      sacc[kt] = zero16();
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const u32x4 k = kt == cx.th ? kb[c][kk] : cx.kx_other[(2 * c + kk) * 64 + lane];
+          sacc[kt] = mfma32(k, qb[c][kk], sacc[kt]);
+        }
+    }
+    f32x16 va[2];  // [head half]: features 32c + j of tokens 8g + 4hh + r
+#pragma unroll
+    for (int c = 0; c < 2; ++c) va[c] = zero16();
+    float m = 0.f, lsum = 0.f;
+    const int L = cx.L, hh = cx.hh;
+    u32x4 a0 = La[lane], a1 = La[16 * 64 + lane];
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      u32x4 n0, n1;
+      if (ks + 1 < 16) {
+        n0 = La[(ks + 1) * 64 + lane];
+        n1 = La[(16 + ks + 1) * 64 + lane];
+      }
+      va[0] = mfma32(bx[ks], a0, va[0]);
+      va[1] = mfma32(bx[ks], a1, va[1]);
+      // softmax units after k-steps 1, 5, 9: the row max over the valid keys, then for each key tile
+      // e = 2^(s - m), its fp32 sum and the bf16 P^T operands
+      if (ks == 1) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          if (32 * kt + 32 <= L) {  // a key tile with no padded keys (uniform): no masking
+#pragma unroll
+            for (int R = 0; R < 16; R += 2) mx = fmaxf(fmaxf(mx, sacc[kt][R]), sacc[kt][R + 1]);
+          } else {
+#pragma unroll
+            for (int R = 0; R < 16; ++R)
+              if (32 * kt + acc_row(R, hh) < L) mx = fmaxf(mx, sacc[kt][R]);
+          }
+        }
+        m = halfwave_max(mx);
+      } else if (ks == 5 || ks == 9) {
+        const int kt = ks == 5 ? 0 : 1;
+        float e[16];
+        if (32 * kt + 32 <= L) {
+#pragma unroll
+          for (int R = 0; R < 16; ++R) e[R] = __builtin_amdgcn_exp2f(sacc[kt][R] - m);
+        } else {
+#pragma unroll
+          for (int R = 0; R < 16; ++R)
+            e[R] = 32 * kt + acc_row(R, hh) < L ? __builtin_amdgcn_exp2f(sacc[kt][R] - m) : 0.f;
+        }
+#pragma unroll
+        for (int R = 0; R < 16; ++R) lsum += e[R];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          cy.pb[2 * kt + kk] = u32x4{pk_bf16(e[8 * kk], e[8 * kk + 1]), pk_bf16(e[8 * kk + 2], e[8 * kk + 3]),
+                                     pk_bf16(e[8 * kk + 4], e[8 * kk + 5]), pk_bf16(e[8 * kk + 6], e[8 * kk + 7])};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < 16) {
+        a0 = n0;
+        a1 = n1;
+      }
+    }
+    // V^T operands of this half's keys [feature tile c][key k-step kk], kept and written to LDS
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const f32x16& v = va[c];
+        cy.vb[c][kk] = u32x4{pk_bf16(v[8 * kk], v[8 * kk + 1]), pk_bf16(v[8 * kk + 2], v[8 * kk + 3]),
+                             pk_bf16(v[8 * kk + 4], v[8 * kk + 5]), pk_bf16(v[8 * kk + 6], v[8 * kk + 7])};
+        cx.vx_own[(2 * c + kk) * 64 + lane] = cy.vb[c][kk];
+      }
+    // gate of head h for this query: in this lane if h / 4 == hh, else in the partner lane
+    float own = cx.gv[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) own = (h & 3) == r ? cx.gv[r] : own;
+    const float other = __shfl_xor(own, 32);
+    const float ls = lsum + __shfl_xor(lsum, 32);
+    cy.sc = (hh == (h >> 2) ? own : other) * (1.0f / ls);
+    cy.off = cx.qoff;
+  }
+}
+
+__global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t* __restrict__ xn,
+                                                                  const u32x4* __restrict__ wq,
+                                                                  const float* __restrict__ bgate,
+                                                                  const float* __restrict__ rope, int mode,
+                                                                  int nseq, int L, int T, int F,
+                                                                  uint16_t* __restrict__ O) {
+  __shared__ u32x4 smem[kFsLdsVecs];  // one LDS object: 2 weight stages, K / V^T exchange
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int j = lane & 31, hh = lane >> 5;
+  const int sl = wave & (kFsSeqs - 1), th = wave >> 2;  // sequence slot, position half
+  const int s = blockIdx.x * kFsSeqs + sl;
+  FsCtx cx;
+  cx.wq = wq;
+  cx.kx_own = smem + kFsOffKx + (2 * sl + th) * 4 * 64;
+  cx.kx_other = smem + kFsOffKx + (2 * sl + (th ^ 1)) * 4 * 64;
+  cx.vx_own = smem + kFsOffVx + (2 * sl + th) * 4 * 64;
+  cx.vx_other = smem + kFsOffVx + (2 * sl + (th ^ 1)) * 4 * 64;
+  cx.active = s < nseq;  // idle waves still stage weights and meet every barrier
+  cx.L = L;
+  cx.p = 32 * th + j;
+  cx.th = th;
+  cx.hh = hh;
+  cx.lane = lane;
+  cx.wave = wave;
+
+  fs_issue(0, smem, wq, wave, lane);
+  const bool valid = cx.active && cx.p < L;
+  {  // rotary table [cos | sin][L][32] fp32 (zero past L)
+    const float* cr = rope + int64_t(valid ? cx.p : 0) * 32;
+    const float* sr = cr + int64_t(L) * 32;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i = 16 * c + 4 * g + 2 * hh;
+        cx.rope.cs[c][g] = valid ? *reinterpret_cast<const float2*>(cr + i) : float2{0.f, 0.f};
+        cx.rope.sn[c][g] = valid ? *reinterpret_cast<const float2*>(sr + i) : float2{0.f, 0.f};
+      }
+  }
+  u32x4 bx[16];  // xn of this lane's position (zero past L), natural k order
+  {
+    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? token_of(mode, s, cx.p, T, F) : 0) * kDim);
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
+  }
+  // O of this sequence as a buffer: token of position p at byte (token_of(p) - token_of(0)) * 1 KB
+  const int64_t tok0 = cx.active ? token_of(mode, s, 0, T, F) : 0;
+  const int tok_stride = mode == 0 ? F : 1;
+  cx.ores = buffer_rsrc(O + tok0 * (kHeads * kHeadDim),
+                        cx.active ? ((L - 1) * tok_stride + 1) * kHeads * kHeadDim * 2 : 0);
+  cx.qoff = cx.p < L ? cx.p * tok_stride * (kHeads * kHeadDim * 2) : kFsDropped;
+  fs_barrier<0>();     // the gate tile
+
+  // ---- the gate tile (stage 0, buffer 0): rows 0..7 live in register group 0 of both half-waves
+  fs_issue(1, smem + kFsStageBlocks * 64, wq, wave, lane);
+  if (cx.active) {
+    f32x16 ga = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) ga = mfma32(smem[ks * 64 + lane], bx[ks], ga);
+    const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) cx.gv[r] = 1.0f / (1.0f + expf(-(ga[r] + bg[r])));
+  }
+
+  // The carry into head 0 is a dummy: its P.V is zero and its stores are all dropped, so that every
+  // head issues the same 8 stores.
+  FsCarry cy;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) cy.vb[c][kk] = zero4();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cy.pb[i] = zero4();
+  cy.sc = 0.f;
+  cy.off = kFsDropped;
+  if (cx.active) {  // the dummy's V^T blocks: P.V of head 0's Aq stage reads the other half's
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cx.vx_own[i * 64 + lane] = zero4();
   }
 #pragma unroll 1
-  for (int h = 0; h < kHeads; ++h) {
-    // ---- stage A: q, k of both halves, rotary, S^T
-    f32x16 sacc[2][2];
-    if (active) {
-      f32x16 qa0[2], ka0[2], qa1[2], ka1[2];
-      u32x4 qb[2][2][2], kb[2][2][2];  // [half][column tile][k-step of the half]
-      fs_qk_half(La, 0, bx, lane, qa0, ka0, [&](int ks) { fs_store_unit(pd, ks, h - 1, hh, ores); });
-      fs_qk_half(La, 1, bx, lane, qa1, ka1, [&](int ks) {
-        if (ks & 1) {
-          const int u = ks >> 1, t = u >> 2, g = u & 3;
-          fs_rotate(qa0[t], ka0[t], ropeL, 0, t, g, j, hh, qb[0][t][g >> 1], kb[0][t][g >> 1]);
-        }
-      });
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          sacc[kt][qt] = zero16();
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) sacc[kt][qt] = mfma32(kb[0][kt][kk], qb[0][qt][kk], sacc[kt][qt]);
-        }
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        fs_rotate(qa1[u >> 2], ka1[u >> 2], ropeL, 1, u >> 2, u & 3, j, hh, qb[1][u >> 2][(u & 3) >> 1],
-                  kb[1][u >> 2][(u & 3) >> 1]);
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) sacc[kt][qt] = mfma32(kb[1][kt][kk], qb[1][qt][kk], sacc[kt][qt]);
-    }
-    // stage B of head h has landed (its loads are older than the 16 stores issued above)
-    if (active)
-      vmcnt_barrier<kFsStoresPerHead>();
-    else
-      vmcnt_barrier<0>();
-    if (h + 1 < kHeads) fs_issue_a(h + 1, La, wq, wave, lane);
-    if (active) {
-      // ---- stage B: v (swapped product, tokens on the rows) with the softmax of S^T between its MFMAs
-      f32x16 va[2][2];  // [head half][token tile]
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) va[c][t] = zero16();
-      float m[2], lsum[2] = {0.f, 0.f};
-      u32x4 pb[2][4];  // P^T operands [query tile][key k-step]
-      u32x4 av0 = Lb[lane], av1 = Lb[16 * 64 + lane];
-#pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {
-        u32x4 n0, n1;
-        if (ks + 1 < 16) {
-          n0 = Lb[(ks + 1) * 64 + lane];
-          n1 = Lb[(16 + ks + 1) * 64 + lane];
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) va[0][t] = mfma32(bx[t][ks], av0, va[0][t]);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) va[1][t] = mfma32(bx[t][ks], av1, va[1][t]);
-        // softmax unit: query tile qt, step st (0: row max over the valid keys; 1, 2: e = 2^(s - m) of key
-        // tile st - 1, its fp32 sum and bf16 P)
-        if ((ks & 1) && ks < 12) {
-          const int u = ks >> 1, qt = u / 3, st = u % 3;
-          if (st == 0) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-              if (32 * kt + 32 <= L) {  // a key tile with no padded keys (uniform): no masking
-#pragma unroll
-                for (int R = 0; R < 16; R += 2) mx = fmaxf(fmaxf(mx, sacc[kt][qt][R]), sacc[kt][qt][R + 1]);
-              } else {
-#pragma unroll
-                for (int R = 0; R < 16; ++R)
-                  if (32 * kt + acc_row(R, hh) < L) mx = fmaxf(mx, sacc[kt][qt][R]);
-              }
-            }
-            m[qt] = halfwave_max(mx);
-          } else {
-            const int kt = st - 1;
-            float e[16];
-            if (32 * kt + 32 <= L) {
-#pragma unroll
-              for (int R = 0; R < 16; ++R) e[R] = __builtin_amdgcn_exp2f(sacc[kt][qt][R] - m[qt]);
-            } else {
-#pragma unroll
-              for (int R = 0; R < 16; ++R)
-                e[R] = 32 * kt + acc_row(R, hh) < L ? __builtin_amdgcn_exp2f(sacc[kt][qt][R] - m[qt]) : 0.f;
-            }
-#pragma unroll
-            for (int R = 0; R < 16; ++R) lsum[qt] += e[R];
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-              pb[qt][2 * kt + kk] = u32x4{pk_bf16(e[8 * kk], e[8 * kk + 1]), pk_bf16(e[8 * kk + 2], e[8 * kk + 3]),
-                                          pk_bf16(e[8 * kk + 4], e[8 * kk + 5]), pk_bf16(e[8 * kk + 6], e[8 * kk + 7])};
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (ks + 1 < 16) {
-          av0 = n0;
-          av1 = n1;
-        }
-      }
-      u32x4 vb[2][4];  // V^T operands [head half = feature tile][key k-step 2 tt + kk]
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            const f32x16& v = va[c][t];
-            vb[c][2 * t + kk] = u32x4{pk_bf16(v[8 * kk], v[8 * kk + 1]), pk_bf16(v[8 * kk + 2], v[8 * kk + 3]),
-                                      pk_bf16(v[8 * kk + 4], v[8 * kk + 5]), pk_bf16(v[8 * kk + 6], v[8 * kk + 7])};
-          }
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          pd.o[dt][qt] = zero16();
-#pragma unroll
-          for (int kv = 0; kv < 4; ++kv) pd.o[dt][qt] = mfma32(vb[dt][kv], pb[qt][kv], pd.o[dt][qt]);
-        }
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        // gate of head h for this query: in this lane if h / 4 == hh, else in the partner lane
-        float own = gv[qt][0];
-#pragma unroll
-        for (int r = 1; r < 4; ++r) own = (h & 3) == r ? gv[qt][r] : own;
-        const float other = __shfl_xor(own, 32);
-        const float ls = lsum[qt] + __shfl_xor(lsum[qt], 32);
-        pd.sc[qt] = (hh == (h >> 2) ? own : other) * (1.0f / ls);
-        pd.off[qt] = qoff[qt];
-      }
-    }
-    // stage A of head h + 1 has landed (the stores of head h - 1 went out during stage A of head h)
-    vmcnt_barrier<0>();
-    if (h + 1 < kHeads) fs_issue_b(h + 1, Lb, wq, wave, lane);
+  for (int h = 0; h < kHeads; h += 2) {
+    fs_head<1>(h, cx, smem, bx, cy);
+    fs_head<0>(h + 1, cx, smem, bx, cy);
   }
-  if (active) {
+  fs_barrier<0>();  // V^T of the last head written by both halves
+  if (cx.active) {
+    FsOut po;
+    fs_pv(cy, cx.vx_other, th, lane, po);
 #pragma unroll
-    for (int u = 0; u < kFsStoresPerHead; ++u) fs_store_unit(pd, u, kHeads - 1, hh, ores);
+    for (int u = 0; u < kFsStoresPerHead; ++u) fs_store_unit(po, u, kHeads - 1, hh, cx.ores);
   }
 }
 
 void launch_qkv_attn_short(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
                            uint16_t* O, hipStream_t st, const LaunchEvents& ev) {
-  const unsigned blocks = unsigned((sh.nseq + kFsWaves - 1) / kFsWaves);
+  const unsigned blocks = unsigned((sh.nseq + kFsSeqs - 1) / kFsSeqs);
   hipExtLaunchKernelGGL(k_qkv_attn_short, dim3(blocks), dim3(64 * kFsWaves), 0, st, ev.start, ev.stop, 0, xn,
-                     reinterpret_cast<const u32x4*>(layer + kOffQkvg),
-                     reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.T, sh.F, O);
+                        reinterpret_cast<const u32x4*>(layer + kOffQkvg),
+                        reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.T, sh.F,
+                        O);
 }
 
 }  // namespace trf
