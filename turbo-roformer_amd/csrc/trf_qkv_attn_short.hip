@@ -10,17 +10,18 @@
 // MFMAs.  A wave keeps its 32 positions' xn rows in registers (bf16, natural k order) and computes q, k
 // and v of its own positions; each half writes its K and V^T operand blocks to LDS and reads the other
 // half's, so that every wave attends its 32 queries over all 64 keys.  A workgroup is 4 sequences (8
-// waves).  The 49 weight tiles of W_qkvg stream through a 2-deep LDS ring of 32 KB stages: the gate tile,
-// then per head the q tiles, the k tiles and the v tiles.
+// waves).  The 49 weight tiles of W_qkvg stream through LDS: the gate tile, then per head stage A (the q
+// and k tiles, 64 KB) and stage B (the v tiles, 32 KB), each in its own buffer so that one loads while the
+// other is read (160 KB of LDS with the exchange blocks).
 //
-// Per head h (stages Aq, Ak, B):
-//   Aq: P.V of head h - 1 (its V^T now visible from both halves) and its 8 bounds-checked O stores,
-//       spread between the q products of head h;
-//   Ak: the k products, with the rotary of q between them; then the rotary of k, written to LDS;
-//   B:  S^T = K.Q^T over both halves' keys, then the v products with the softmax of S^T between them;
-//       then V^T packed and written to LDS.
+// Per head h:
+//   A: P.V of head h - 1 (its V^T now visible from both halves) and its 8 bounds-checked O stores,
+//      spread between the q products of head h; then the k products with the rotary of q between them;
+//      then the rotary of k, written to LDS;
+//   B: S^T = K.Q^T over both halves' keys, then the v products with the softmax of S^T between them;
+//      then V^T packed and written to LDS.
 // The stage barriers wait for the stage's loads with an exact vmcnt (the 8 O stores of a head are
-// issued after the loads of the following stage and are never waited for) and for the LDS exchange.
+// issued after the loads of stage B and are never waited for) and for the LDS exchange.
 //
 // No data crosses lanes between the projection and the attention:
 //   * q and k come out of C = W . xn^T with lane (j, hh) holding token j of the column tile and features
@@ -38,33 +39,43 @@ namespace trf {
 
 constexpr int kFsSeqs = 4;                       // sequences per workgroup
 constexpr int kFsWaves = 2 * kFsSeqs;            // one wave per 32-position half; waves w, w + 4 share a SIMD
-constexpr int kFsStageBlocks = 32;               // 1 KB operand blocks per weight stage
-constexpr int kFsStages = 1 + 3 * kHeads;        // the gate tile, then q, k and v tiles per head
+constexpr int kFsBlocksA = 64;                   // q and k tiles of a head: 2 kinds x 2 halves x 16 k-steps
+constexpr int kFsBlocksB = 32;                   // v tiles of a head: 2 halves x 16 k-steps
+constexpr int kFsBlocksG = 16;                   // the gate tile (in stage B's buffer)
 constexpr int kFsStoresPerHead = 8;              // O stores per wave and head: 2 feature tiles x 4 groups
-// LDS layout, in 16-byte units: the two weight stages, then the K and V^T operand blocks exchanged
-// between the halves, [sequence][half][k-step][lane] (128 KB).
-constexpr int kFsOffKx = 2 * kFsStageBlocks * 64;
+// LDS layout, in 16-byte units: stage A, stage B, then the K and V^T operand blocks exchanged between
+// the halves, [sequence][half][k-step][lane] (160 KB).
+constexpr int kFsOffB = kFsBlocksA * 64;
+constexpr int kFsOffKx = kFsOffB + kFsBlocksB * 64;
 constexpr int kFsOffVx = kFsOffKx + kFsSeqs * 2 * 4 * 64;
 constexpr int kFsLdsVecs = kFsOffVx + kFsSeqs * 2 * 4 * 64;
 constexpr int kFsDropped = 0x40000000;  // buffer offset past any sequence's output: the store is dropped
 
-// This wave's share of stage n into LDS buffer buf: the gate tile (n = 0: k-step b of the last tile), or
-// for n = 1 + 3h + kind (kind 0 q, 1 k, 2 v) block 16c + ks = k-step ks of tile 16 kind + 2h + c.
-__device__ __forceinline__ void fs_issue(int n, u32x4* buf, const u32x4* wq, int wave, int lane) {
-  if (n >= kFsStages) return;
-  if (n == 0) {
+// This wave's share of the gate tile (the last tile of W_qkvg).
+__device__ __forceinline__ void fs_issue_gate(u32x4* buf, const u32x4* wq, int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int b = 2 * wave + i;
-      lds_load_block(wq + (int64_t(kQkvgTiles - 1) * 16 + b) * 64, buf + b * 64, lane);
-    }
-    return;
+  for (int i = 0; i < kFsBlocksG / kFsWaves; ++i) {
+    const int b = (kFsBlocksG / kFsWaves) * wave + i;
+    lds_load_block(wq + (int64_t(kQkvgTiles - 1) * 16 + b) * 64, buf + b * 64, lane);
   }
-  const int h = (n - 1) / 3, kind = (n - 1) % 3;
+}
+
+// Stage A of head h: block 32 kind + 16 c + ks is k-step ks of tile 16 kind + 2h + c (kind 0 q, 1 k).
+__device__ __forceinline__ void fs_issue_a(int h, u32x4* buf, const u32x4* wq, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < kFsStageBlocks / kFsWaves; ++i) {
-    const int b = (kFsStageBlocks / kFsWaves) * wave + i;
-    const int t = 16 * kind + 2 * h + (b >> 4);
+  for (int i = 0; i < kFsBlocksA / kFsWaves; ++i) {
+    const int b = (kFsBlocksA / kFsWaves) * wave + i;
+    const int t = 16 * (b >> 5) + 2 * h + ((b >> 4) & 1);
+    lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, buf + b * 64, lane);
+  }
+}
+
+// Stage B of head h: block 16 c + ks is k-step ks of v tile 32 + 2h + c.
+__device__ __forceinline__ void fs_issue_b(int h, u32x4* buf, const u32x4* wq, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < kFsBlocksB / kFsWaves; ++i) {
+    const int b = (kFsBlocksB / kFsWaves) * wave + i;
+    const int t = 32 + 2 * h + (b >> 4);
     lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, buf + b * 64, lane);
   }
 }
@@ -155,55 +166,46 @@ struct FsCtx {
   float gv[4];  // sigmoid gates of heads 4hh + r for this lane's query
 };
 
-// One head: stages Aq (LDS buffer PA), Ak (1 - PA) and B (PA) of stage numbers n, n + 1, n + 2, n = 1 + 3h.
-// The buffer parity is a template argument so that every LDS address is a compile-time constant plus a
-// lane term: the compiler can then tell the operand reads from the direct-to-LDS loads into the other
-// buffer and does not wait for those loads.
-template <int PA>
+// One head: stage A (q and k) and stage B (v, attention).
 __device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, const u32x4 (&bx)[16], FsCarry& cy) {
-  u32x4* const La = smem + PA * kFsStageBlocks * 64;
-  u32x4* const Lk = smem + (1 - PA) * kFsStageBlocks * 64;
-  const int n = 1 + 3 * h, lane = cx.lane;
+  u32x4* const La = smem;
+  u32x4* const Lb = smem + kFsOffB;
+  const int lane = cx.lane;
 
-  // ---- stage Aq: P.V and stores of head h - 1, q products of head h
-  fs_barrier<0>();  // q tiles landed; V^T of head h - 1 written by both halves
-  fs_issue(n + 1, Lk, cx.wq, cx.wave, lane);
-  f32x16 qa[2];
-  if (cx.active) {
-    FsOut po;
-    fs_pv(cy, cx.vx_other, cx.th, lane, po);  // for h = 0 a dummy whose stores are all dropped
-#pragma unroll
-    for (int c = 0; c < 2; ++c) qa[c] = zero16();
-    u32x4 a0 = La[lane], a1 = La[16 * 64 + lane];
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-      u32x4 n0, n1;
-      if (ks + 1 < 16) {
-        n0 = La[(ks + 1) * 64 + lane];
-        n1 = La[(16 + ks + 1) * 64 + lane];
-      }
-      qa[0] = mfma32(a0, bx[ks], qa[0]);
-      qa[1] = mfma32(a1, bx[ks], qa[1]);
-      if (ks & 1) fs_store_unit(po, ks >> 1, h - 1, cx.hh, cx.ores);
-      __builtin_amdgcn_sched_barrier(0);
-      if (ks + 1 < 16) {
-        a0 = n0;
-        a1 = n1;
-      }
-    }
-  }
-
-  // ---- stage Ak: k products with the rotary of q between them, then the rotary of k into LDS
-  if (cx.active)
-    fs_barrier<kFsStoresPerHead>();  // k tiles landed (the 8 stores above are younger)
-  else
-    fs_barrier<0>();
-  fs_issue(n + 2, La, cx.wq, cx.wave, lane);
+  // ---- stage A: P.V and stores of head h - 1 between the q products of head h, then the k products
+  // with the rotary of q between them, then the rotary of k into LDS
+  fs_barrier<0>();  // stage A landed; V^T of head h - 1 written by both halves
+  fs_issue_b(h, Lb, cx.wq, cx.wave, lane);
   u32x4 qb[2][2], kb[2][2];  // [head half][k-step of the half]
   if (cx.active) {
+    f32x16 qa[2];
+    {
+      FsOut po;
+      fs_pv(cy, cx.vx_other, cx.th, lane, po);  // for h = 0 a dummy whose stores are all dropped
+#pragma unroll
+      for (int c = 0; c < 2; ++c) qa[c] = zero16();
+      u32x4 a0 = La[lane], a1 = La[16 * 64 + lane];
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        u32x4 n0, n1;
+        if (ks + 1 < 16) {
+          n0 = La[(ks + 1) * 64 + lane];
+          n1 = La[(16 + ks + 1) * 64 + lane];
+        }
+        qa[0] = mfma32(a0, bx[ks], qa[0]);
+        qa[1] = mfma32(a1, bx[ks], qa[1]);
+        if (ks & 1) fs_store_unit(po, ks >> 1, h - 1, cx.hh, cx.ores);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < 16) {
+          a0 = n0;
+          a1 = n1;
+        }
+      }
+    }
     f32x16 ka[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) ka[c] = zero16();
+    const u32x4* const Lk = La + 32 * 64;
     u32x4 a0 = Lk[lane], a1 = Lk[16 * 64 + lane];
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) {
@@ -233,8 +235,11 @@ __device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, con
   }
 
   // ---- stage B: S^T over both halves' keys, v products with the softmax between them, V^T into LDS
-  fs_barrier<0>();  // v tiles landed; K written by both halves
-  fs_issue(n + 3, Lk, cx.wq, cx.wave, lane);
+  if (cx.active)
+    fs_barrier<kFsStoresPerHead>();  // stage B landed (the 8 stores above are younger); K written
+  else
+    fs_barrier<0>();
+  if (h + 1 < kHeads) fs_issue_a(h + 1, La, cx.wq, cx.wave, lane);
   if (cx.active) {
     f32x16 sacc[2];  // [key tile]
 #pragma unroll
@@ -253,13 +258,13 @@ __device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, con
     for (int c = 0; c < 2; ++c) va[c] = zero16();
     float m = 0.f, lsum = 0.f;
     const int L = cx.L, hh = cx.hh;
-    u32x4 a0 = La[lane], a1 = La[16 * 64 + lane];
+    u32x4 a0 = Lb[lane], a1 = Lb[16 * 64 + lane];
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) {
       u32x4 n0, n1;
       if (ks + 1 < 16) {
-        n0 = La[(ks + 1) * 64 + lane];
-        n1 = La[(16 + ks + 1) * 64 + lane];
+        n0 = Lb[(ks + 1) * 64 + lane];
+        n1 = Lb[(16 + ks + 1) * 64 + lane];
       }
       va[0] = mfma32(bx[ks], a0, va[0]);
       va[1] = mfma32(bx[ks], a1, va[1]);
@@ -330,7 +335,7 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
                                                                   const float* __restrict__ rope, int mode,
                                                                   int nseq, int L, int T, int F,
                                                                   uint16_t* __restrict__ O) {
-  __shared__ u32x4 smem[kFsLdsVecs];  // one LDS object: 2 weight stages, K / V^T exchange
+  __shared__ u32x4 smem[kFsLdsVecs];  // one LDS object: stage A, stage B, K / V^T exchange
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int sl = wave & (kFsSeqs - 1), th = wave >> 2;  // sequence slot, position half
@@ -349,7 +354,8 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
   cx.lane = lane;
   cx.wave = wave;
 
-  fs_issue(0, smem, wq, wave, lane);
+  fs_issue_gate(smem + kFsOffB, wq, wave, lane);
+  fs_issue_a(0, smem, wq, wave, lane);
   const bool valid = cx.active && cx.p < L;
   {  // rotary table [cos | sin][L][32] fp32 (zero past L)
     const float* cr = rope + int64_t(valid ? cx.p : 0) * 32;
@@ -375,14 +381,13 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
   cx.ores = buffer_rsrc(O + tok0 * (kHeads * kHeadDim),
                         cx.active ? ((L - 1) * tok_stride + 1) * kHeads * kHeadDim * 2 : 0);
   cx.qoff = cx.p < L ? cx.p * tok_stride * (kHeads * kHeadDim * 2) : kFsDropped;
-  fs_barrier<0>();     // the gate tile
+  fs_barrier<0>();     // the gate tile and stage A of head 0
 
-  // ---- the gate tile (stage 0, buffer 0): rows 0..7 live in register group 0 of both half-waves
-  fs_issue(1, smem + kFsStageBlocks * 64, wq, wave, lane);
+  // ---- the gate tile (in stage B's buffer): rows 0..7 live in register group 0 of both half-waves
   if (cx.active) {
     f32x16 ga = zero16();
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) ga = mfma32(smem[ks * 64 + lane], bx[ks], ga);
+    for (int ks = 0; ks < 16; ++ks) ga = mfma32(smem[kFsOffB + ks * 64 + lane], bx[ks], ga);
     const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
 #pragma unroll
     for (int r = 0; r < 4; ++r) cx.gv[r] = 1.0f / (1.0f + expf(-(ga[r] + bg[r])));
@@ -404,10 +409,7 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
     for (int i = 0; i < 4; ++i) cx.vx_own[i * 64 + lane] = zero4();
   }
 #pragma unroll 1
-  for (int h = 0; h < kHeads; h += 2) {
-    fs_head<1>(h, cx, smem, bx, cy);
-    fs_head<0>(h + 1, cx, smem, bx, cy);
-  }
+  for (int h = 0; h < kHeads; ++h) fs_head(h, cx, smem, bx, cy);
   fs_barrier<0>();  // V^T of the last head written by both halves
   if (cx.active) {
     FsOut po;
