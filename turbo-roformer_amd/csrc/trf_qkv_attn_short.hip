@@ -14,6 +14,11 @@
 // and k tiles, 64 KB) and stage B (the v tiles, 32 KB), each in its own buffer so that one loads while the
 // other is read (160 KB of LDS with the exchange blocks).
 //
+// Work is dealt in units of (group of 4 sequences, head): workgroup b of G runs units [bU/G, (b+1)U/G)
+// of the U = 8 x groups in order, so one workgroup per CU gets an even share of heads (13 or 14 units
+// for the 1701 frames of a 17 s chunk) instead of two rounds of whole groups (1.66 groups per CU).  A
+// group entered mid-way or left early loads its xn rows and computes its gates again.
+//
 // Per head h:
 //   A: P.V of head h - 1 (its V^T now visible from both halves) and its 8 bounds-checked O stores,
 //      spread between the q products of head h; then the k products with the rotary of q between them;
@@ -33,6 +38,8 @@
 //     A operand (V^T) of O^T = V^T . P^T with the keys of a k-step in the register order in which the
 //     S^T accumulator holds them, so P^T is the B operand straight from the accumulator.
 // The row max and the row sum combine the two half-waves (the query's keys sit in lanes j and j + 32).
+#include <atomic>
+
 #include "trf_device.h"
 
 namespace trf {
@@ -166,8 +173,10 @@ struct FsCtx {
   float gv[4];  // sigmoid gates of heads 4hh + r for this lane's query
 };
 
-// One head: stage A (q and k) and stage B (v, attention).
-__device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, const u32x4 (&bx)[16], FsCarry& cy) {
+// One head: stage A (q and k) and stage B (v, attention).  hn is the head of the workgroup's next unit
+// (its stage A is loaded during stage B), or -1.
+__device__ __forceinline__ void fs_head(int h, int hn, const FsCtx& cx, u32x4* smem, const u32x4 (&bx)[16],
+                                        FsCarry& cy) {
   u32x4* const La = smem;
   u32x4* const Lb = smem + kFsOffB;
   const int lane = cx.lane;
@@ -239,7 +248,7 @@ __device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, con
     fs_barrier<kFsStoresPerHead>();  // stage B landed (the 8 stores above are younger); K written
   else
     fs_barrier<0>();
-  if (h + 1 < kHeads) fs_issue_a(h + 1, La, cx.wq, cx.wave, lane);
+  if (hn >= 0) fs_issue_a(hn, La, cx.wq, cx.wave, lane);
   if (cx.active) {
     f32x16 sacc[2];  // [key tile]
 #pragma unroll
@@ -329,6 +338,17 @@ __device__ __forceinline__ void fs_head(int h, const FsCtx& cx, u32x4* smem, con
   }
 }
 
+// The last head's P.V and stores of a group, once both halves have written its V^T.
+__device__ __forceinline__ void fs_flush(const FsCtx& cx, const FsCarry& cy, int h) {
+  fs_barrier<0>();
+  if (cx.active) {
+    FsOut po;
+    fs_pv(cy, cx.vx_other, cx.th, cx.lane, po);
+#pragma unroll
+    for (int u = 0; u < kFsStoresPerHead; ++u) fs_store_unit(po, u, h, cx.hh, cx.ores);
+  }
+}
+
 __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t* __restrict__ xn,
                                                                   const u32x4* __restrict__ wq,
                                                                   const float* __restrict__ bgate,
@@ -339,91 +359,116 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int sl = wave & (kFsSeqs - 1), th = wave >> 2;  // sequence slot, position half
-  const int s = blockIdx.x * kFsSeqs + sl;
+  const int units = (nseq + kFsSeqs - 1) / kFsSeqs * kHeads;
+  const int u_begin = int(int64_t(blockIdx.x) * units / gridDim.x);
+  const int u_end = int(int64_t(blockIdx.x + 1) * units / gridDim.x);
   FsCtx cx;
   cx.wq = wq;
   cx.kx_own = smem + kFsOffKx + (2 * sl + th) * 4 * 64;
   cx.kx_other = smem + kFsOffKx + (2 * sl + (th ^ 1)) * 4 * 64;
   cx.vx_own = smem + kFsOffVx + (2 * sl + th) * 4 * 64;
   cx.vx_other = smem + kFsOffVx + (2 * sl + (th ^ 1)) * 4 * 64;
-  cx.active = s < nseq;  // idle waves still stage weights and meet every barrier
   cx.L = L;
   cx.p = 32 * th + j;
   cx.th = th;
   cx.hh = hh;
   cx.lane = lane;
   cx.wave = wave;
+  const int tok_stride = mode == 0 ? F : 1;
+  // the output row of this lane's position within its sequence (kFsDropped past the sequence end)
+  cx.qoff = cx.p < L ? cx.p * tok_stride * (kHeads * kHeadDim * 2) : kFsDropped;
 
-  fs_issue_gate(smem + kFsOffB, wq, wave, lane);
-  fs_issue_a(0, smem, wq, wave, lane);
-  const bool valid = cx.active && cx.p < L;
-  {  // rotary table [cos | sin][L][32] fp32 (zero past L)
-    const float* cr = rope + int64_t(valid ? cx.p : 0) * 32;
+  fs_issue_a(u_begin % kHeads, smem, wq, wave, lane);
+  {  // rotary table [cos | sin][L][32] fp32, for this lane's position in every sequence (zero past L)
+    const bool in = cx.p < L;
+    const float* cr = rope + int64_t(in ? cx.p : 0) * 32;
     const float* sr = cr + int64_t(L) * 32;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int i = 16 * c + 4 * g + 2 * hh;
-        cx.rope.cs[c][g] = valid ? *reinterpret_cast<const float2*>(cr + i) : float2{0.f, 0.f};
-        cx.rope.sn[c][g] = valid ? *reinterpret_cast<const float2*>(sr + i) : float2{0.f, 0.f};
+        cx.rope.cs[c][g] = in ? *reinterpret_cast<const float2*>(cr + i) : float2{0.f, 0.f};
+        cx.rope.sn[c][g] = in ? *reinterpret_cast<const float2*>(sr + i) : float2{0.f, 0.f};
       }
   }
-  u32x4 bx[16];  // xn of this lane's position (zero past L), natural k order
-  {
-    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? token_of(mode, s, cx.p, T, F) : 0) * kDim);
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
-  }
-  // O of this sequence as a buffer: token of position p at byte (token_of(p) - token_of(0)) * 1 KB
-  const int64_t tok0 = cx.active ? token_of(mode, s, 0, T, F) : 0;
-  const int tok_stride = mode == 0 ? F : 1;
-  cx.ores = buffer_rsrc(O + tok0 * (kHeads * kHeadDim),
-                        cx.active ? ((L - 1) * tok_stride + 1) * kHeads * kHeadDim * 2 : 0);
-  cx.qoff = cx.p < L ? cx.p * tok_stride * (kHeads * kHeadDim * 2) : kFsDropped;
-  fs_barrier<0>();     // the gate tile and stage A of head 0
-
-  // ---- the gate tile (in stage B's buffer): rows 0..7 live in register group 0 of both half-waves
-  if (cx.active) {
-    f32x16 ga = zero16();
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) ga = mfma32(smem[kFsOffB + ks * 64 + lane], bx[ks], ga);
-    const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) cx.gv[r] = 1.0f / (1.0f + expf(-(ga[r] + bg[r])));
-  }
-
-  // The carry into head 0 is a dummy: its P.V is zero and its stores are all dropped, so that every
-  // head issues the same 8 stores.
   FsCarry cy;
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) cy.vb[c][kk] = zero4();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) cy.pb[i] = zero4();
-  cy.sc = 0.f;
-  cy.off = kFsDropped;
-  if (cx.active) {  // the dummy's V^T blocks: P.V of head 0's Aq stage reads the other half's
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cx.vx_own[i * 64 + lane] = zero4();
-  }
+  int h_last = 0;
 #pragma unroll 1
-  for (int h = 0; h < kHeads; ++h) fs_head(h, cx, smem, bx, cy);
-  fs_barrier<0>();  // V^T of the last head written by both halves
-  if (cx.active) {
-    FsOut po;
-    fs_pv(cy, cx.vx_other, th, lane, po);
+  for (int u = u_begin; u < u_end;) {
+    const int grp = u / kHeads, h0 = u - grp * kHeads;
+    const int h1 = min(kHeads, h0 + (u_end - u));  // this group's heads h0 .. h1 - 1
+    if (u != u_begin) fs_flush(cx, cy, h_last);    // the previous group's last head
+    fs_issue_gate(smem + kFsOffB, wq, wave, lane);
+    const int s = grp * kFsSeqs + sl;
+    cx.active = s < nseq;  // idle waves still stage weights and meet every barrier
+    const bool valid = cx.active && cx.p < L;
+    u32x4 bx[16];  // xn of this lane's position (zero past L), natural k order
+    {
+      const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? token_of(mode, s, cx.p, T, F) : 0) * kDim);
 #pragma unroll
-    for (int u = 0; u < kFsStoresPerHead; ++u) fs_store_unit(po, u, kHeads - 1, hh, cx.ores);
+      for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
+    }
+    // O of this sequence as a buffer: token of position p at byte (token_of(p) - token_of(0)) * 1 KB
+    const int64_t tok0 = cx.active ? token_of(mode, s, 0, T, F) : 0;
+    cx.ores = buffer_rsrc(O + tok0 * (kHeads * kHeadDim),
+                          cx.active ? ((L - 1) * tok_stride + 1) * kHeads * kHeadDim * 2 : 0);
+    fs_barrier<0>();  // the gate tile, stage A of head h0 and xn
+
+    // ---- the gate tile (in stage B's buffer): rows 0..7 live in register group 0 of both half-waves
+    if (cx.active) {
+      f32x16 ga = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) ga = mfma32(smem[kFsOffB + ks * 64 + lane], bx[ks], ga);
+      const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) cx.gv[r] = 1.0f / (1.0f + expf(-(ga[r] + bg[r])));
+    }
+
+    // The carry into head h0 is a dummy: its P.V is zero and its stores are all dropped, so that every
+    // head issues the same 8 stores.
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) cy.vb[c][kk] = zero4();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cy.pb[i] = zero4();
+    cy.sc = 0.f;
+    cy.off = kFsDropped;
+    if (cx.active) {  // the dummy's V^T blocks: P.V of head h0's stage A reads the other half's
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cx.vx_own[i * 64 + lane] = zero4();
+    }
+#pragma unroll 1
+    for (int h = h0; h < h1; ++h) {
+      const int next = grp * kHeads + h + 1;  // the next unit, if this workgroup has one
+      fs_head(h, next < u_end ? (h + 1) % kHeads : -1, cx, smem, bx, cy);
+    }
+    h_last = h1 - 1;
+    u += h1 - h0;
   }
+  if (u_end > u_begin) fs_flush(cx, cy, h_last);
+}
+
+// Workgroups of the fused kernel: one per CU (the kernel deals its units itself), at most one per unit.
+static int fs_grid(int nseq) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  const int units = (nseq + kFsSeqs - 1) / kFsSeqs * kHeads;
+  return units < n ? units : n;
 }
 
 void launch_qkv_attn_short(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
                            uint16_t* O, hipStream_t st, const LaunchEvents& ev) {
-  const unsigned blocks = unsigned((sh.nseq + kFsSeqs - 1) / kFsSeqs);
-  hipExtLaunchKernelGGL(k_qkv_attn_short, dim3(blocks), dim3(64 * kFsWaves), 0, st, ev.start, ev.stop, 0, xn,
-                        reinterpret_cast<const u32x4*>(layer + kOffQkvg),
+  if (sh.nseq <= 0) return;
+  hipExtLaunchKernelGGL(k_qkv_attn_short, dim3(unsigned(fs_grid(sh.nseq))), dim3(64 * kFsWaves), 0, st, ev.start,
+                        ev.stop, 0, xn, reinterpret_cast<const u32x4*>(layer + kOffQkvg),
                         reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.T, sh.F,
                         O);
 }
