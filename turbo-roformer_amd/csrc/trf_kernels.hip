@@ -13,6 +13,8 @@
 // for every GEMM/attention operand (kernels.cpp:30-33).
 #include "trf_device.h"
 
+#include <atomic>
+
 #include <type_traits>
 
 namespace trf {
@@ -160,9 +162,14 @@ void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_
 //
 // A stage runs as two groups of two tiles (two interleaved MFMA chains each).  A group's outputs
 // leave as 8 packed 8-byte stores per lane, issued during the NEXT group's MFMA loop, one every other
-// k-step, so the write stream runs under the matrix work instead of in a burst between stages (every
-// workgroup reaches its epilogue at about the same time).  Stage barriers wait with an exact vmcnt for
-// the weight loads issued before those stores.
+// k-step, so the write stream runs under the matrix work instead of in a burst between stages.  Stage
+// barriers wait with an exact vmcnt for the weight loads issued before those stores.
+//
+// Work is dealt in units of (block of 256 rows, stage): workgroup b of G runs units [bU/G, (b+1)U/G) of
+// the U = 13 x blocks in order, so one workgroup per CU gets an even share of stages (21 or 22 for the
+// 419 blocks of a 17 s chunk's time sub-layer) instead of two rounds of whole blocks (1.64 per CU).  A
+// block entered mid-way loads its xn rows and rotary table again; one left early stores its last group
+// at once.
 constexpr int kQkvWaves = 8;
 constexpr int kQkvTps = 4;
 constexpr int kQkvStages = (kQkvgTiles + kQkvTps - 1) / kQkvTps;
@@ -170,63 +177,16 @@ constexpr int kQkvGroupStores = 8;  // 2 tiles x 4 register groups
 
 __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
                                                   const float* __restrict__ bgate, const float* __restrict__ rope,
-                                                  int mode, int nseq, int L, int Lpad, int T, int F,
+                                                  int mode, int nseq, int L, int Lpad, int T, int F, int nblocks,
                                                   uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
                                                   uint16_t* __restrict__ Vt, float* __restrict__ G) {
   __shared__ u32x4 lds[2][kQkvTps * 16 * 64];  // 2 stages x 4 tiles x 16 k-steps x 1 KB
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
-  const int64_t row0 = (int64_t(blockIdx.x) * kQkvWaves + wave) * 32;
-  const bool active = row0 < int64_t(nseq) * Lpad;  // inactive waves still stage weights and meet barriers
-  const int s = active ? int(row0 / Lpad) : 0;
-  const int p = active ? int(row0 % Lpad) + j : 0;
-  const bool valid = active && p < L;
-  const int64_t tok = valid ? token_of(mode, s, p, T, F) : 0;
-
-  u32x4 bx[16];
-  {
-    const u32x4* xr = reinterpret_cast<const u32x4*>(xn + tok * kDim);
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
-  }
-  // Rotary of this position: features d0 = 32 half + 8g + 4hh (+0..3) form the pairs
-  // i = 16 half + 4g + 2hh + c, c = 0, 1.  rope = [cos | sin] rows of 32.
-  float2 rc[2][4], rsn[2][4];
-  {
-    const float* cr = rope + int64_t(valid ? p : 0) * 32;
-    const float* sr = cr + int64_t(L) * 32;
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        rc[half][g] = *reinterpret_cast<const float2*>(cr + 16 * half + 4 * g + 2 * hh);
-        rsn[half][g] = *reinterpret_cast<const float2*>(sr + 16 * half + 4 * g + 2 * hh);
-      }
-  }
-
-  // q/k rows are chunk-major: features 8c..8c+7 of position p at ((s*8 + h)*8 + c)*Lpad + p, so the 32
-  // lanes of a half-wave store 32 consecutive 16-byte chunks (hh fills bytes 8hh..8hh+7).
-  const int64_t qk_off = (int64_t(s) * kHeads * 8 * Lpad + p) * 8 + 4 * hh;
-  // V^T rows: lane 4q + r of a half-wave stores row r of its register group at positions 4q..4q+3
+  const int units = nblocks * kQkvStages;
+  const int u_begin = int(int64_t(blockIdx.x) * units / gridDim.x);
+  const int u_end = int(int64_t(blockIdx.x + 1) * units / gridDim.x);
   const int qd = lane & 3;
-  const int64_t v_off = (int64_t(s) * kHeads * kHeadDim + 4 * hh + qd) * Lpad + (p & ~3);
-  u32x2 pend[kQkvGroupStores];  // the previous group's packed outputs
-
-  // Store i of the outputs of group grp of stage ps: tile 4ps + 2grp + i/4, register group i%4.  Every
-  // offset beyond the lane's own is wave-uniform.
-  auto store_pending = [&](int ps, int grp, int i) __attribute__((always_inline)) {
-    const int tt = 2 * grp + (i >> 2), g = i & 3, t = kQkvTps * ps + tt, half = tt & 1;
-    if (ps < 8) {
-      const int h = (t & 15) >> 1;
-      uint16_t* base = (ps < 4 ? Q : K) + qk_off;
-      const int64_t off = int64_t(__builtin_amdgcn_readfirstlane((h * 8 + 4 * half + g) * Lpad)) * 8;
-      *reinterpret_cast<u32x2*>(base + off) = pend[i];
-    } else {
-      const int h = (t - 32) >> 1;
-      const int drow = h * kHeadDim + 32 * half + 8 * g;  // row of V^T, less 4hh + r
-      *reinterpret_cast<u32x2*>(Vt + v_off + int64_t(__builtin_amdgcn_readfirstlane(drow * Lpad))) = pend[i];
-    }
-  };
 
   auto issue = [&](int stage, int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -236,117 +196,195 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
       if (t < kQkvgTiles) lds_load_block(wq + (int64_t(t) * 16 + (b & 15)) * 64, &lds[buf][b * 64], lane);
     }
   };
-  issue(0, 0);
-  // Everything loaded so far has landed (the first stage barrier waits for it anyway): stated as the
-  // builtin so that the compiler's own waitcnt insertion, which cannot tell the barrier branches below
-  // apart, adds no waits for the xn and rotary registers inside the loop.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
-  for (int stage = 0; stage < kQkvStages; ++stage) {
-    // This stage's weight loads were issued at the top of the previous stage, whose two loops then
-    // issued 8 stores each (only the second loop at stage 0).
-    if (active && stage >= 2)
-      vmcnt_barrier<2 * kQkvGroupStores>();
-    else if (active && stage == 1)
-      vmcnt_barrier<kQkvGroupStores>();
-    else
-      vmcnt_barrier<0>();
-    if (stage + 1 < kQkvStages) issue(stage + 1, (stage + 1) & 1);
-    if (!active) continue;
-    const u32x4* Ls = lds[stage & 1];
-    if (stage == kQkvStages - 1) {  // the gate tile: rows 0..7 live in register group 0 of both half-waves
-      f32x16 acc = zero16();
+  issue(u_begin % kQkvStages, u_begin & 1);
+
+#pragma unroll 1
+  for (int u = u_begin; u < u_end;) {
+    const int blk = u / kQkvStages, st0 = u - blk * kQkvStages;
+    const int st1 = min(kQkvStages, st0 + (u_end - u));  // this block's stages st0 .. st1 - 1
+    const int64_t row0 = (int64_t(blk) * kQkvWaves + wave) * 32;
+    const bool active = row0 < int64_t(nseq) * Lpad;  // inactive waves still stage weights and meet barriers
+    const int s = active ? int(row0 / Lpad) : 0;
+    const int p = active ? int(row0 % Lpad) + j : 0;
+    const bool valid = active && p < L;
+    const int64_t tok = valid ? token_of(mode, s, p, T, F) : 0;
+
+    u32x4 bx[16];
+    {
+      const u32x4* xr = reinterpret_cast<const u32x4*>(xn + tok * kDim);
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {
-        acc = mfma32(Ls[ks * 64 + lane], bx[ks], acc);
-        if (ks & 1) store_pending(stage - 1, 1, ks >> 1);
-      }
-      if (valid) {
-        const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
-        f32x4 gv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) gv[r] = 1.0f / (1.0f + expf(-(acc[r] + bg[r])));
-        *reinterpret_cast<f32x4*>(G + tok * kHeads + 4 * hh) = gv;
-      }
-      continue;
+      for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();
     }
+    // Rotary of this position: features d0 = 32 half + 8g + 4hh (+0..3) form the pairs
+    // i = 16 half + 4g + 2hh + c, c = 0, 1.  rope = [cos | sin] rows of 32.
+    float2 rc[2][4], rsn[2][4];
+    {
+      const float* cr = rope + int64_t(valid ? p : 0) * 32;
+      const float* sr = cr + int64_t(L) * 32;
 #pragma unroll
-    for (int grp = 0; grp < 2; ++grp) {
-      f32x16 acc[2];
-      u32x4 a[2];
+      for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        acc[u] = zero16();
-        a[u] = Ls[(2 * grp + u) * 16 * 64 + lane];
-      }
-      const bool pending = grp == 1 || stage > 0;
-#pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {  // operands of k-step ks+1 are read while ks multiplies
-        u32x4 an[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-          if (ks + 1 < 16) an[u] = Ls[((2 * grp + u) * 16 + ks + 1) * 64 + lane];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) acc[u] = mfma32(a[u], bx[ks], acc[u]);
-        if ((ks & 1) && pending) store_pending(grp ? stage : stage - 1, grp ^ 1, ks >> 1);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-          if (ks + 1 < 16) a[u] = an[u];
-      }
-      if (stage < 8) {  // q (stages 0-3) or k (4-7): rotate interleaved pairs in fp32, pack bf16 rows
-        // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
-        const float sc = stage < 4 ? kLog2e : 1.0f;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int half = u;  // tiles 2grp and 2grp+1 are halves 0 and 1 of one head
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float2 c = rc[half][g], sn = rsn[half][g];
-            const float a0 = acc[u][4 * g], a1 = acc[u][4 * g + 1], a2 = acc[u][4 * g + 2], a3 = acc[u][4 * g + 3];
-            u32x2 o = {0u, 0u};
-            if (valid) {
-              o[0] = pk_bf16(fmaf(a0, c.x, -(a1 * sn.x)) * sc, fmaf(a1, c.x, a0 * sn.x) * sc);
-              o[1] = pk_bf16(fmaf(a2, c.y, -(a3 * sn.y)) * sc, fmaf(a3, c.y, a2 * sn.y) * sc);
-            }
-            pend[4 * u + g] = o;
-          }
+        for (int g = 0; g < 4; ++g) {
+          rc[half][g] = *reinterpret_cast<const float2*>(cr + 16 * half + 4 * g + 2 * hh);
+          rsn[half][g] = *reinterpret_cast<const float2*>(sr + 16 * half + 4 * g + 2 * hh);
         }
-      } else {  // v: register group g holds rows 8g + 4hh + r (r = 0..3) of position p; a 4 x 4
-        // transpose across each lane quad (two DPP exchanges) leaves lane 4q + r with row r of
-        // positions 4q..4q+3, so a half-wave's store covers 4 rows x 64 contiguous bytes.
-        const bool b1 = qd & 2, b0 = qd & 1;
-        // byte selectors of v_perm_b32 (bytes 0-3 from the second operand, 4-7 from the first)
-        const uint32_t sel_send = b0 ? 0x05040100u : 0x07060302u;
-        const uint32_t sel_f0 = b0 ? 0x03020504u : 0x05040100u;
-        const uint32_t sel_f1 = b0 ? 0x03020706u : 0x07060100u;
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            // d0/d1: rows (0,1)/(2,3) of this position (zero past the sequence end)
-            const uint32_t d0 = valid ? pk_bf16(acc[u][4 * g], acc[u][4 * g + 1]) : 0u;
-            const uint32_t d1 = valid ? pk_bf16(acc[u][4 * g + 2], acc[u][4 * g + 3]) : 0u;
-            // exchange with lane ^ 2: lanes 0,1 keep rows 0,1 of positions q, q+2; lanes 2,3 rows 2,3
-            const uint32_t r1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(b1 ? d0 : d1), 0x4E, 0xF, 0xF, true));
-            const uint32_t e0 = b1 ? r1 : d0, e1 = b1 ? d1 : r1;
-            // exchange halves with lane ^ 1: lane r ends with row r of positions 0..3
-            const uint32_t snd = __builtin_amdgcn_perm(e1, e0, sel_send);
-            const uint32_t r2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(snd), 0xB1, 0xF, 0xF, true));
-            pend[4 * u + g] = u32x2{__builtin_amdgcn_perm(r2, e0, sel_f0), __builtin_amdgcn_perm(r2, e1, sel_f1)};
-          }
+    }
+
+    // q/k rows are chunk-major: features 8c..8c+7 of position p at ((s*8 + h)*8 + c)*Lpad + p, so the 32
+    // lanes of a half-wave store 32 consecutive 16-byte chunks (hh fills bytes 8hh..8hh+7).
+    const int64_t qk_off = (int64_t(s) * kHeads * 8 * Lpad + p) * 8 + 4 * hh;
+    // V^T rows: lane 4q + r of a half-wave stores row r of its register group at positions 4q..4q+3
+    const int64_t v_off = (int64_t(s) * kHeads * kHeadDim + 4 * hh + qd) * Lpad + (p & ~3);
+    u32x2 pend[kQkvGroupStores];  // the previous group's packed outputs
+
+    // Store i of the outputs of group grp of stage ps: tile 4ps + 2grp + i/4, register group i%4.  Every
+    // offset beyond the lane's own is wave-uniform.
+    auto store_pending = [&](int ps, int grp, int i) __attribute__((always_inline)) {
+      const int tt = 2 * grp + (i >> 2), g = i & 3, t = kQkvTps * ps + tt, half = tt & 1;
+      if (ps < 8) {
+        const int h = (t & 15) >> 1;
+        uint16_t* base = (ps < 4 ? Q : K) + qk_off;
+        const int64_t off = int64_t(__builtin_amdgcn_readfirstlane((h * 8 + 4 * half + g) * Lpad)) * 8;
+        *reinterpret_cast<u32x2*>(base + off) = pend[i];
+      } else {
+        const int h = (t - 32) >> 1;
+        const int drow = h * kHeadDim + 32 * half + 8 * g;  // row of V^T, less 4hh + r
+        *reinterpret_cast<u32x2*>(Vt + v_off + int64_t(__builtin_amdgcn_readfirstlane(drow * Lpad))) = pend[i];
       }
+    };
+    // Everything loaded so far has landed (the block's first stage barrier waits for it anyway): stated
+    // as the builtin so that the compiler's own waitcnt insertion, which cannot tell the barrier branches
+    // below apart, adds no waits for the xn and rotary registers inside the stage loop.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+#pragma unroll 1
+    for (int stage = st0; stage < st1; ++stage, ++u) {
+      // This stage's weight loads were issued at the top of the previous unit, whose two loops then
+      // issued 8 stores each (only the second loop in a block's first stage); a block's first stage
+      // follows the xn and rotary loads and waits for everything.
+      if (active && stage >= st0 + 2)
+        vmcnt_barrier<2 * kQkvGroupStores>();
+      else if (active && stage == st0 + 1)
+        vmcnt_barrier<kQkvGroupStores>();
+      else
+        vmcnt_barrier<0>();
+      if (u + 1 < u_end) issue((u + 1) % kQkvStages, (u + 1) & 1);
+      if (!active) continue;
+      const u32x4* Ls = lds[u & 1];
+      if (stage == kQkvStages - 1) {  // the gate tile: rows 0..7 live in register group 0 of both half-waves
+        f32x16 acc = zero16();
+        const bool pending = stage > st0;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+          acc = mfma32(Ls[ks * 64 + lane], bx[ks], acc);
+          if ((ks & 1) && pending) store_pending(stage - 1, 1, ks >> 1);
+        }
+        if (valid) {
+          const f32x4 bg = *reinterpret_cast<const f32x4*>(bgate + 4 * hh);
+          f32x4 gv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) gv[r] = 1.0f / (1.0f + expf(-(acc[r] + bg[r])));
+          *reinterpret_cast<f32x4*>(G + tok * kHeads + 4 * hh) = gv;
+        }
+        continue;
+      }
+#pragma unroll
+      for (int grp = 0; grp < 2; ++grp) {
+        f32x16 acc[2];
+        u32x4 a[2];
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+          acc[v] = zero16();
+          a[v] = Ls[(2 * grp + v) * 16 * 64 + lane];
+        }
+        const bool pending = grp == 1 || stage > st0;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {  // operands of k-step ks+1 are read while ks multiplies
+          u32x4 an[2];
+#pragma unroll
+          for (int v = 0; v < 2; ++v)
+            if (ks + 1 < 16) an[v] = Ls[((2 * grp + v) * 16 + ks + 1) * 64 + lane];
+#pragma unroll
+          for (int v = 0; v < 2; ++v) acc[v] = mfma32(a[v], bx[ks], acc[v]);
+          if ((ks & 1) && pending) store_pending(grp ? stage : stage - 1, grp ^ 1, ks >> 1);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int v = 0; v < 2; ++v)
+            if (ks + 1 < 16) a[v] = an[v];
+        }
+        if (stage < 8) {  // q (stages 0-3) or k (4-7): rotate interleaved pairs in fp32, pack bf16 rows
+          // q leaves in units of log2(e) (scores become base-2 exponents for the softmax); k as is
+          const float sc = stage < 4 ? kLog2e : 1.0f;
+#pragma unroll
+          for (int v = 0; v < 2; ++v) {
+            const int half = v;  // tiles 2grp and 2grp+1 are halves 0 and 1 of one head
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const float2 c = rc[half][g], sn = rsn[half][g];
+              const float a0 = acc[v][4 * g], a1 = acc[v][4 * g + 1], a2 = acc[v][4 * g + 2], a3 = acc[v][4 * g + 3];
+              u32x2 o = {0u, 0u};
+              if (valid) {
+                o[0] = pk_bf16(fmaf(a0, c.x, -(a1 * sn.x)) * sc, fmaf(a1, c.x, a0 * sn.x) * sc);
+                o[1] = pk_bf16(fmaf(a2, c.y, -(a3 * sn.y)) * sc, fmaf(a3, c.y, a2 * sn.y) * sc);
+              }
+              pend[4 * v + g] = o;
+            }
+          }
+        } else {  // v: register group g holds rows 8g + 4hh + r (r = 0..3) of position p; a 4 x 4
+          // transpose across each lane quad (two DPP exchanges) leaves lane 4q + r with row r of
+          // positions 4q..4q+3, so a half-wave's store covers 4 rows x 64 contiguous bytes.
+          const bool b1 = qd & 2, b0 = qd & 1;
+          // byte selectors of v_perm_b32 (bytes 0-3 from the second operand, 4-7 from the first)
+          const uint32_t sel_send = b0 ? 0x05040100u : 0x07060302u;
+          const uint32_t sel_f0 = b0 ? 0x03020504u : 0x05040100u;
+          const uint32_t sel_f1 = b0 ? 0x03020706u : 0x07060100u;
+#pragma unroll
+          for (int v = 0; v < 2; ++v)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              // d0/d1: rows (0,1)/(2,3) of this position (zero past the sequence end)
+              const uint32_t d0 = valid ? pk_bf16(acc[v][4 * g], acc[v][4 * g + 1]) : 0u;
+              const uint32_t d1 = valid ? pk_bf16(acc[v][4 * g + 2], acc[v][4 * g + 3]) : 0u;
+              // exchange with lane ^ 2: lanes 0,1 keep rows 0,1 of positions q, q+2; lanes 2,3 rows 2,3
+              const uint32_t r1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(b1 ? d0 : d1), 0x4E, 0xF, 0xF, true));
+              const uint32_t e0 = b1 ? r1 : d0, e1 = b1 ? d1 : r1;
+              // exchange halves with lane ^ 1: lane r ends with row r of positions 0..3
+              const uint32_t snd = __builtin_amdgcn_perm(e1, e0, sel_send);
+              const uint32_t r2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(snd), 0xB1, 0xF, 0xF, true));
+              pend[4 * v + g] = u32x2{__builtin_amdgcn_perm(r2, e0, sel_f0), __builtin_amdgcn_perm(r2, e1, sel_f1)};
+            }
+        }
+      }
+    }
+    // a block left before its gate stage: its last group's outputs leave now
+    if (active && st1 < kQkvStages) {
+#pragma unroll
+      for (int i = 0; i < kQkvGroupStores; ++i) store_pending(st1 - 1, 1, i);
     }
   }
+}
+
+// Workgroups of the QKV kernel: one per CU (the kernel deals its units itself), at most one per unit.
+static int qkv_grid(int units) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return units < n ? units : n;
 }
 
 void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh, uint16_t* Q,
                 uint16_t* K, uint16_t* Vt, float* G, hipStream_t st, const LaunchEvents& ev) {
   const int64_t rows = int64_t(sh.nseq) * sh.Lpad;
-  const unsigned blocks = unsigned((rows / 32 + kQkvWaves - 1) / kQkvWaves);
-  hipExtLaunchKernelGGL(k_qkv_rope, dim3(blocks), dim3(64 * kQkvWaves), 0, st, ev.start, ev.stop, 0, xn,
-                     reinterpret_cast<const u32x4*>(layer + kOffQkvg),
-                     reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.Lpad,
-                     sh.T, sh.F, Q, K, Vt, G);
+  const int nblocks = int((rows / 32 + kQkvWaves - 1) / kQkvWaves);
+  if (nblocks <= 0) return;
+  hipExtLaunchKernelGGL(k_qkv_rope, dim3(unsigned(qkv_grid(nblocks * kQkvStages))), dim3(64 * kQkvWaves), 0, st,
+                        ev.start, ev.stop, 0, xn, reinterpret_cast<const u32x4*>(layer + kOffQkvg),
+                        reinterpret_cast<const float*>(layer + kOffBgate), rope, sh.mode, sh.nseq, sh.L, sh.Lpad,
+                        sh.T, sh.F, nblocks, Q, K, Vt, G);
 }
 
 
