@@ -99,7 +99,9 @@ def test_qkv_rope_gemm(hip, layers, mode, batch, T, F):
     assert (Q.cpu()[:, :, :, L:] == 0).all() and (K.cpu()[:, :, :, L:] == 0).all() and (Vt.cpu()[..., L:] == 0).all()
 
 
-ATT_SHAPES = QKV_SHAPES + [(0, 1, 1700, 2), (0, 1, 200, 9), (1, 3, 11, 64)]
+# (0, 1, 300, 100): 1,600 workgroups of time attention (three rounds on 256 CUs at two per CU); the second
+# query block of each sequence has one wave with queries and three without.
+ATT_SHAPES = QKV_SHAPES + [(0, 1, 1700, 2), (0, 1, 200, 9), (1, 3, 11, 64), (0, 1, 300, 100)]
 
 
 @pytest.mark.parametrize("mode,batch,T,F", ATT_SHAPES)
@@ -130,18 +132,20 @@ def test_attention(hip, layers, mode, batch, T, F):
     assert snr_db(exact.view(n, 512).numpy(), O.double().cpu().numpy()) >= 40.0
 
 
-def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers):
+@pytest.mark.parametrize("T,F,key", [(900, 2, 700), (400, 64, 300)])
+def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers, T, F, key):
     """Long sequences are swept with a fixed integer shift from the first 32 keys; a score far above it
-    overflows that sweep's sums, and the workgroup redoes the sweep with the raised-shift method.  Here the
-    32 queries 96..127 of every (sequence, head) are a multiple of key 700, so their scores on it are ~100
-    (base 2) above the rest: the result must still be the softmax."""
+    overflows that sweep's sums, and the sweep is redone with the raised-shift method.  Here the 32 queries
+    96..127 of every (sequence, head) are a multiple of one key, so their scores on it are ~100 (base 2)
+    above the rest: the result must still be the softmax.  With F = 64, 512 of the 1,024 workgroups redo
+    their sweep."""
     w, _ = layers[0]
-    mode, batch, T, F = 0, 1, 900, 2
+    mode, batch = 0, 1
     n = batch * T * F
     xn = ok.l2_rows(rand_x(n, 77)).to(torch.bfloat16)
     Q, K, Vt, G = ok.qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], mode, batch, T, F)
-    K[:, :, :, 700, :] = 4.0
-    Q[:, :, :, 96:128, :] = 100.0 / (64 * 16.0) * 4.0  # q . k_700 = 64 * 4 * 0.39 = 100
+    K[:, :, :, key, :] = 4.0
+    Q[:, :, :, 96:128, :] = 100.0 / (64 * 16.0) * 4.0  # q . k_key = 64 * 4 * 0.39 = 100
     Oref = ok.attention(Q, K, Vt, G, mode, batch, T, F)
     O = torch.empty(n, 512, dtype=torch.bfloat16, device=DEV)
     print("attention with a dominant key (guarded sweep)", flush=True)
@@ -149,12 +153,12 @@ def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers)
     torch.cuda.synchronize()
     assert torch.isfinite(O.float()).all()
     assert_bf16_close(Oref, O, "O", min_snr=48)
-    # the spiked queries attend to key 700 alone: O = gate * V[700]
+    # the spiked queries attend to the one key alone: O = gate * V[key]
     idx = ok.token_index(mode, batch, T, F)  # [nseq, L] token of (sequence, position)
     for s_ in range(idx.shape[0]):
         tok = idx[s_, 100]
-        v700 = Vt[s_, :, :, 700].float()  # [8 heads, 64]
-        want = (G[tok].float()[:, None] * v700).reshape(512)
+        vk = Vt[s_, :, :, key].float()  # [8 heads, 64]
+        want = (G[tok].float()[:, None] * vk).reshape(512)
         torch.testing.assert_close(O[tok].float().cpu(), want, rtol=1e-2, atol=1e-3)
 
 
