@@ -78,7 +78,9 @@ QKV_SHAPES = [  # (mode, batch, T, F)
 ]
 
 
-@pytest.mark.parametrize("mode,batch,T,F", QKV_SHAPES)
+# (0, 1, 1701, 40): 270 blocks of 256 rows, 3,510 (block, stage) units, so each of the kernel's
+# workgroups (one per CU) runs 13-14 stages back to back across block boundaries.
+@pytest.mark.parametrize("mode,batch,T,F", QKV_SHAPES + [(0, 1, 1701, 40)])
 def test_qkv_rope_gemm(hip, layers, mode, batch, T, F):
     w, packed = layers[mode]
     n = batch * T * F
