@@ -133,7 +133,7 @@ __device__ __forceinline__ void fs_store_unit(const FsOut& po, int u, int h, int
   __builtin_amdgcn_raw_buffer_store_b64(v, ores, off, 0, 0);
 }
 
-// What one head leaves for the next stage Aq: this half's V^T operands [feature tile][key k-step], the
+// What one head leaves for the next head's stage A: this half's V^T operands [feature tile][key k-step], the
 // P^T operands of its queries [key k-step 2 kt + kk], and the scale and offset of its output.
 struct FsCarry {
   u32x4 vb[2][2];
@@ -174,7 +174,9 @@ struct FsCtx {
 };
 
 // One head: stage A (q and k) and stage B (v, attention).  hn is the head of the workgroup's next unit
-// (its stage A is loaded during stage B), or -1.
+// (its stage A is loaded during stage B), or -1.  CARRY: the previous head of the same group was run
+// here, and its P.V and stores happen in this head's stage A.
+template <bool CARRY>
 __device__ __forceinline__ void fs_head(int h, int hn, const FsCtx& cx, u32x4* smem, const u32x4 (&bx)[16],
                                         FsCarry& cy) {
   u32x4* const La = smem;
@@ -190,7 +192,7 @@ __device__ __forceinline__ void fs_head(int h, int hn, const FsCtx& cx, u32x4* s
     f32x16 qa[2];
     {
       FsOut po;
-      fs_pv(cy, cx.vx_other, cx.th, lane, po);  // for h = 0 a dummy whose stores are all dropped
+      if (CARRY) fs_pv(cy, cx.vx_other, cx.th, lane, po);
 #pragma unroll
       for (int c = 0; c < 2; ++c) qa[c] = zero16();
       u32x4 a0 = La[lane], a1 = La[16 * 64 + lane];
@@ -203,7 +205,7 @@ __device__ __forceinline__ void fs_head(int h, int hn, const FsCtx& cx, u32x4* s
         }
         qa[0] = mfma32(a0, bx[ks], qa[0]);
         qa[1] = mfma32(a1, bx[ks], qa[1]);
-        if (ks & 1) fs_store_unit(po, ks >> 1, h - 1, cx.hh, cx.ores);
+        if (CARRY && (ks & 1)) fs_store_unit(po, ks >> 1, h - 1, cx.hh, cx.ores);
         __builtin_amdgcn_sched_barrier(0);
         if (ks + 1 < 16) {
           a0 = n0;
@@ -244,7 +246,7 @@ __device__ __forceinline__ void fs_head(int h, int hn, const FsCtx& cx, u32x4* s
   }
 
   // ---- stage B: S^T over both halves' keys, v products with the softmax between them, V^T into LDS
-  if (cx.active)
+  if (cx.active && CARRY)
     fs_barrier<kFsStoresPerHead>();  // stage B landed (the 8 stores above are younger); K written
   else
     fs_barrier<0>();
@@ -425,24 +427,15 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
       for (int r = 0; r < 4; ++r) cx.gv[r] = 1.0f / (1.0f + expf(-(ga[r] + bg[r])));
     }
 
-    // The carry into head h0 is a dummy: its P.V is zero and its stores are all dropped, so that every
-    // head issues the same 8 stores.
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) cy.vb[c][kk] = zero4();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cy.pb[i] = zero4();
-    cy.sc = 0.f;
-    cy.off = kFsDropped;
-    if (cx.active) {  // the dummy's V^T blocks: P.V of head h0's stage A reads the other half's
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cx.vx_own[i * 64 + lane] = zero4();
+    // head h0 has no previous head to finish; the others finish theirs in their stage A
+    {
+      const int next = grp * kHeads + h0 + 1;  // the next unit, if this workgroup has one
+      fs_head<false>(h0, next < u_end ? (h0 + 1) % kHeads : -1, cx, smem, bx, cy);
     }
 #pragma unroll 1
-    for (int h = h0; h < h1; ++h) {
-      const int next = grp * kHeads + h + 1;  // the next unit, if this workgroup has one
-      fs_head(h, next < u_end ? (h + 1) % kHeads : -1, cx, smem, bx, cy);
+    for (int h = h0 + 1; h < h1; ++h) {
+      const int next = grp * kHeads + h + 1;
+      fs_head<true>(h, next < u_end ? (h + 1) % kHeads : -1, cx, smem, bx, cy);
     }
     h_last = h1 - 1;
     u += h1 - h0;
