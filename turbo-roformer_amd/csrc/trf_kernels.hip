@@ -157,7 +157,7 @@ void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_
 // One wave owns 32 consecutive padded positions of one sequence; its 32 tokens' xn rows stay in
 // registers as B operands.  The workgroup (8 waves, 2 per SIMD) streams the 49 weight tiles through
 // LDS four per stage (13 stages: q heads, k heads, v heads, then the gate tile), so every stage is of
-// one kind.  The rotary cos/sin of the wave's position is loaded into registers once.
+// one kind.  The rotary cos/sin of the wave's position is loaded into registers with its xn rows.
 // (kernels.cpp:439-540)
 //
 // A stage runs as two groups of two tiles (two interleaved MFMA chains each).  A group's outputs
