@@ -34,6 +34,10 @@ SHAPES = [  # (mode, batch, T, F)
     (0, 1, 64, 3),
     (0, 1, 40, 5),
     (0, 2, 1, 5),
+    # group and head splits between the kernel's workgroups (one per CU, an even share of
+    # (4-sequence group, head) units each): 3 x 257 = 771 sequences (1,544 units), 2 x 129 = 258 (520)
+    (1, 3, 257, 64),
+    (1, 2, 129, 45),
 ]
 
 
