@@ -88,6 +88,9 @@ void launch_pack_f16(const uint16_t* hi, const uint16_t* lo, int rows, int K, ui
 void launch_copy_f32(const float* src, int n, float* dst, hipStream_t st);
 void launch_add_rmsnorm(float* X, const void* Y, int y_bf16, void* out, int out_bf16, int64_t n,
                         float eps, hipStream_t st);
+// CUs of the current device (hipDeviceAttributeMultiprocessorCount, cached per device): the grid of the
+// kernels that deal their work units themselves, one workgroup per CU.
+int device_cu_count();
 void launch_qkv(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
                 uint16_t* Q, uint16_t* K, uint16_t* Vt, float* G, hipStream_t st, const LaunchEvents& ev = {});
 void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,

@@ -363,8 +363,7 @@ __global__ __launch_bounds__(512) void k_qkv_rope(const uint16_t* __restrict__ x
   }
 }
 
-// Workgroups of the QKV kernel: one per CU (the kernel deals its units itself), at most one per unit.
-static int qkv_grid(int units) {
+int device_cu_count() {
   static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -373,6 +372,12 @@ static int qkv_grid(int units) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     cus[dev].store(n, std::memory_order_relaxed);
   }
+  return n;
+}
+
+// Workgroups of the QKV kernel: one per CU (the kernel deals its units itself), at most one per unit.
+static int qkv_grid(int units) {
+  const int n = device_cu_count();
   return units < n ? units : n;
 }
 

@@ -38,8 +38,6 @@
 //     A operand (V^T) of O^T = V^T . P^T with the keys of a k-step in the register order in which the
 //     S^T accumulator holds them, so P^T is the B operand straight from the accumulator.
 // The row max and the row sum combine the two half-waves (the query's keys sit in lanes j and j + 32).
-#include <atomic>
-
 #include "trf_device.h"
 
 namespace trf {
@@ -445,14 +443,7 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_qkv_attn_short(const uint16_t
 
 // Workgroups of the fused kernel: one per CU (the kernel deals its units itself), at most one per unit.
 static int fs_grid(int nseq) {
-  static std::atomic<int> cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int n = cus[dev].load(std::memory_order_relaxed);
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev].store(n, std::memory_order_relaxed);
-  }
+  const int n = device_cu_count();
   const int units = (nseq + kFsSeqs - 1) / kFsSeqs * kHeads;
   return units < n ? units : n;
 }
