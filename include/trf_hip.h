@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define TRF_ABI_VERSION 7
+#define TRF_ABI_VERSION 8
 
 #define TRF_DIM 256
 #define TRF_HEADS 8
@@ -158,16 +158,27 @@ int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, cons
 int trf_qkv_attention_short(const uint16_t* xn, const void* packed_layer, const float* rope, int32_t mode,
                             int32_t batch, int32_t T, int32_t F, uint16_t* O, trf_stream_t stream);
 
-/* X += A @ W^T (+ bias); xn = X / max(|X|, eps) as bf16.  which = 0: out-projection
- * (A = O [n][512], no bias); which = 1: FF2 (A = H [n][1024], bias b_ff2).
- * Replaces gemm_res_norm (kernels.cpp:542-586). */
-int trf_gemm_res_norm(const uint16_t* A, const void* packed_layer, int32_t which, float* X,
+/* Bytes of one weight matrix W [rows][K] packed by trf_pack_weight (0 for a bad shape). */
+size_t trf_weight_packed_bytes(int32_t rows, int32_t K);
+
+/* Pack a bf16 weight W [rows][K] (row-major, device; K a multiple of 16) into the MFMA operand tiles
+ * that trf_gemm_res_norm and trf_gemm_gelu read (rows padded with zeros to a multiple of 32), into
+ * packed (device, trf_weight_packed_bytes(rows, K)).  Replaces _pack_w (fast.py:43-49), which builds
+ * the reference ops' P["Wop"], P["W1p"] and P["W2p"] (fast.py:182-189). */
+int trf_pack_weight(const uint16_t* W, int32_t rows, int32_t K, void* packed, trf_stream_t stream);
+
+/* gemm_res_norm(A, Wp, bias, X, xn, eps): X += A @ W^T (+ bias); xn = X / max(|X|, eps) as bf16.
+ * A bf16 [n_rows][K] (K a multiple of 16: 512 for the out-projection, 1024 for FF2), W packed by
+ * trf_pack_weight with rows = 256, bias fp32 [256] or NULL, X fp32 [n_rows][256] updated in place,
+ * xn bf16 [n_rows][256].  Replaces gemm_res_norm (kernels.cpp:542-586). */
+int trf_gemm_res_norm(const uint16_t* A, int32_t K, const void* w_packed, const float* bias, float* X,
                       uint16_t* xn, int64_t n_rows, float eps, trf_stream_t stream);
 
-/* H = gelu_erf(xn @ W1^T + b1), bf16 [n][1024].  Replaces gemm_gelu (kernels.cpp:609-642)
- * and the oneDNN FF1 (fast.py:343-346). */
-int trf_gemm_gelu(const uint16_t* xn, const void* packed_layer, uint16_t* H, int64_t n_rows,
-                  trf_stream_t stream);
+/* gemm_gelu(xn, Wp, bias, H): H = gelu_erf(xn @ W^T + bias) as bf16.  xn bf16 [n_rows][256], W packed by
+ * trf_pack_weight with rows = n_out and K = 256 (n_out a multiple of 32), bias fp32 [n_out], H bf16
+ * [n_rows][n_out].  Replaces gemm_gelu (kernels.cpp:609-642) and the oneDNN FF1 (fast.py:343-346). */
+int trf_gemm_gelu(const uint16_t* xn, const void* w_packed, const float* bias, int32_t n_out, uint16_t* H,
+                  int64_t n_rows, trf_stream_t stream);
 
 /* ---------------------------------------------------------------- stack */
 
@@ -199,7 +210,10 @@ int trf_stack_forward(float* X, int32_t batch, int32_t T, int32_t F,
  * trf_stack_workspace_bytes exceed the array fail with TRF_ERR_WORKSPACE.  All calls on one GPU share
  * that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (other streams
  * or threads) race, so the caller serialises them.  Nothing in the array has to start at zero: every
- * workspace element a call reads, the same call wrote first. */
+ * workspace element a call reads, the same call wrote first.  Under HIP graph capture: the first call
+ * on a device (which looks the array's address up) must happen outside the capture; later calls
+ * capture as plain kernel launches.  The array is part of the library's code object, so every process
+ * that launches any of the library's kernels on a GPU holds it there, whether or not it calls this. */
 int trf_stack_forward_static(float* X, int32_t batch, int32_t T, int32_t F,
                              const void* const* packed_layers, const int32_t* modes, int32_t n_layers,
                              int32_t precision, const float* rope_time, const float* rope_freq,

@@ -121,34 +121,29 @@ std::vector<bf16> pack_panels(const float* W, int O, int K, int nc) {
   return out;
 }
 
-// acc[r][v] = sum over k of A[r][k] * B[k][16 v + lane]: rows a[0..5] (bf16, k pairs read as 32-bit
-// broadcasts), B one panel [kp][16 NV][2].
-// The sums live in a local array (registers) and are written to acc once: accumulating into acc itself
-// makes the compiler store all 24 accumulators on every k step.
+// Register tile of the GEMMs: out[r][v] = sum over k pairs j of rows[r][2j..2j+1] . panel[j][16 v + lane][0..1],
+// six A rows (bf16) against one panel of NV 16-column vectors ([kp][16 NV][2] bf16), fp32 sums.
+// Per k pair the six row pairs are broadcast into registers first; each panel vector is then loaded once
+// and met by all six of them.  The 6 x NV sums stay in registers (a local array) and leave once at the end.
 template <int NV>
-inline void mk6(const bf16* const a[6], const bf16* __restrict__ bp, int kp, __m512 acc[6][NV]) {
-  __m512 c[6][NV];
+inline void tile_dot(const bf16* const rows[6], const bf16* __restrict__ panel, int kp, __m512 out[6][NV]) {
+  __m512 sum[NV][6];
+  for (auto& col : sum)
+    for (auto& x : col) x = _mm512_setzero_ps();
+  const __m512i* pv = reinterpret_cast<const __m512i*>(panel);
+  for (int j = 0; j < kp; ++j, pv += NV) {
+    __m512bh pair[6];
 #pragma GCC unroll 6
-  for (int r = 0; r < 6; ++r)
+    for (int r = 0; r < 6; ++r) pair[r] = (__m512bh)_mm512_set1_epi32(ld32(rows[r] + 2 * j));
 #pragma GCC unroll 4
-    for (int v = 0; v < NV; ++v) c[r][v] = _mm512_setzero_ps();
-  const bf16 *a0 = a[0], *a1 = a[1], *a2 = a[2], *a3 = a[3], *a4 = a[4], *a5 = a[5];
-  for (int j = 0; j < kp; ++j) {
-    __m512bh b[NV];
-#pragma GCC unroll 4
-    for (int v = 0; v < NV; ++v) b[v] = (__m512bh)_mm512_loadu_si512(bp + (size_t(j) * NV * 16 + v * 16) * 2);
-    const bf16* ar[6] = {a0, a1, a2, a3, a4, a5};
+    for (int v = 0; v < NV; ++v) {
+      const __m512bh w = (__m512bh)_mm512_loadu_si512(pv + v);
 #pragma GCC unroll 6
-    for (int r = 0; r < 6; ++r) {
-      const __m512bh av = (__m512bh)_mm512_set1_epi32(ld32(ar[r] + 2 * j));
-#pragma GCC unroll 4
-      for (int v = 0; v < NV; ++v) c[r][v] = _mm512_dpbf16_ps(c[r][v], av, b[v]);
+      for (int r = 0; r < 6; ++r) sum[v][r] = _mm512_dpbf16_ps(sum[v][r], pair[r], w);
     }
   }
-#pragma GCC unroll 6
-  for (int r = 0; r < 6; ++r)
-#pragma GCC unroll 4
-    for (int v = 0; v < NV; ++v) acc[r][v] = c[r][v];
+  for (int v = 0; v < NV; ++v)
+    for (int r = 0; r < 6; ++r) out[r][v] = sum[v][r];
 }
 
 template <class Fn>
@@ -305,7 +300,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
             const bf16* a[6];
             tile_rows(xn.data(), kDim, tr.r0 + m0, rows, a);
             __m512 acc[6][4];
-            mk6<4>(a, panel, kDim / 2, acc);
+            tile_dot<4>(a, panel, kDim / 2, acc);
             for (int r = 0; r < rows; ++r) {
               const int64_t n = tr.r0 + m0 + r;
               int s, i;
@@ -337,7 +332,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
           const bf16* a[6];
           tile_rows(xn.data(), kDim, tr.r0 + m0, rows, a);
           __m512 acc[6][1];
-          mk6<1>(a, P.wg.data(), kDim / 2, acc);
+          tile_dot<1>(a, P.wg.data(), kDim / 2, acc);
           alignas(64) float g[16];
           for (int r = 0; r < rows; ++r) {
             _mm512_store_ps(g, sigmoid_ps(_mm512_add_ps(acc[r][0], _mm512_loadu_ps(P.bg.data()))));
@@ -373,7 +368,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
           for (int r = 0; r < 6; ++r) mx[r] = _mm512_set1_ps(-INFINITY);
           for (int tl = 0; tl < ntile; ++tl) {
             __m512 acc[6][4];
-            mk6<4>(a, kb + int64_t(tl) * 64 * kDh, kDh / 2, acc);
+            tile_dot<4>(a, kb + int64_t(tl) * 64 * kDh, kDh / 2, acc);
             for (int g = 0; g < 4; ++g) {
               const int key0 = tl * 64 + 16 * g;
               const __mmask16 valid = key0 + 16 <= L ? __mmask16(0xffff) : key0 >= L ? __mmask16(0) : __mmask16((1u << (L - key0)) - 1);
@@ -400,7 +395,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
           const bf16* pr[6];
           for (int r = 0; r < 6; ++r) pr[r] = &Pb[std::min(r, rows - 1) * lp];
           __m512 acc[6][4];
-          mk6<4>(pr, vb, (L + 1) / 2, acc);
+          tile_dot<4>(pr, vb, (L + 1) / 2, acc);
           for (int r = 0; r < rows; ++r) {
             const int64_t n = base + int64_t(q0 + r) * stride;
             const __m512 sc = _mm512_set1_ps(inv[r] * gates[n * kGates + head]);
@@ -422,7 +417,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
             const bf16* a[6];
             tile_rows(ao.data(), kH * kDh, tr.r0 + m0, rows, a);
             __m512 acc[6][4];
-            mk6<4>(a, panel, kH * kDh / 2, acc);
+            tile_dot<4>(a, panel, kH * kDh / 2, acc);
             for (int r = 0; r < rows; ++r) {
               float* x = X + (tr.r0 + m0 + r) * kDim + p * 64;
               for (int vv = 0; vv < 4; ++vv) _mm512_storeu_ps(x + 16 * vv, _mm512_add_ps(_mm512_loadu_ps(x + 16 * vv), acc[r][vv]));
@@ -444,7 +439,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
             const bf16* a[6];
             tile_rows(xn.data(), kDim, tr.r0 + m0, rows, a);
             __m512 acc[6][4];
-            mk6<4>(a, panel, kDim / 2, acc);
+            tile_dot<4>(a, panel, kDim / 2, acc);
             for (int r = 0; r < rows; ++r) {
               bf16* o = h.data() + (tr.r0 + m0 + r) * kFf + p * 64;
               for (int vv = 0; vv < 4; ++vv)
@@ -467,7 +462,7 @@ void Stack::forward(float* X, int b, int T, int F, int threads) {
             const bf16* a[6];
             tile_rows(h.data(), kFf, tr.r0 + m0, rows, a);
             __m512 acc[6][4];
-            mk6<4>(a, panel, kFf / 2, acc);
+            tile_dot<4>(a, panel, kFf / 2, acc);
             for (int r = 0; r < rows; ++r) {
               float* x = X + (tr.r0 + m0 + r) * kDim + p * 64;
               for (int vv = 0; vv < 4; ++vv)

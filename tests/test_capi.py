@@ -49,7 +49,14 @@ def test_argument_errors_need_no_device(lib):
     assert b"O must not be NULL" in lib.trf_last_error()
     assert lib.trf_qkv_rope_gemm(p, p, p, 0, 0, 8, 2, p, p, p, p, None) == 1
     assert b"batch" in lib.trf_last_error()
-    assert lib.trf_gemm_res_norm(p, p, 3, p, p, 10, 1e-12, None) == 1
+    assert lib.trf_gemm_res_norm(p, 500, p, None, p, p, 10, 1e-12, None) == 1
+    assert b"multiple of 16" in lib.trf_last_error()
+    assert lib.trf_gemm_gelu(p, p, p, 100, p, 10, None) == 1
+    assert b"multiple of 32" in lib.trf_last_error()
+    assert lib.trf_pack_weight(p, 256, 24, p, None) == 1
+    assert lib.trf_weight_packed_bytes(256, 512) == 8 * 32 * 1024
+    assert lib.trf_weight_packed_bytes(96, 256) == 3 * 16 * 1024
+    assert lib.trf_weight_packed_bytes(256, 24) == 0
     assert lib.trf_stack_forward(p, 1, 8, 2, None, None, 0, 0, None, None, p, 0, None) == 2
     assert b"workspace" in lib.trf_last_error()
     assert lib.trf_stack_forward(p, 1, 8, 2, None, None, 0, 7, None, None, p, 1 << 30, None) == 1

@@ -164,31 +164,43 @@ def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers,
         torch.testing.assert_close(O[tok].float().cpu(), want, rtol=1e-2, atol=1e-3)
 
 
-@pytest.mark.parametrize("which", [0, 1])
+@pytest.mark.parametrize("which", ["out", "ff2", "k256"])
 @pytest.mark.parametrize("n", [1, 31, 1000, 4133])
 def test_gemm_res_norm(hip, layers, which, n):
-    w, packed = layers[0]
-    kd = 512 if which == 0 else 1024
+    """gemm_res_norm(A, Wp, bias?, X, xn, eps) with a standalone packed weight: the out-projection (K = 512,
+    no bias), FF2 (K = 1024, bias) and a K = 256 weight of its own, as the reference op takes any K."""
+    w, _ = layers[0]
+    if which == "k256":
+        g = torch.Generator().manual_seed(7)
+        W, b = (torch.randn(256, 256, generator=g) * 0.05).to(torch.bfloat16), torch.randn(256, generator=g)
+    else:
+        W, b = (w["Wo"], None) if which == "out" else (w["W2"], w["b2"])
+    kd = W.shape[1]
     A = (rand_x(n, 30 + n).repeat(1, kd // 256) * 0.5).to(torch.bfloat16)
     X = rand_x(n, 40 + n, 2.0)
-    Xr, xnr = ok.gemm_res_norm(A, w["Wo"] if which == 0 else w["W2"], None if which == 0 else w["b2"], X)
+    Xr, xnr = ok.gemm_res_norm(A, W, b, X)
     Xd = X.to(DEV)
     xn = torch.empty(n, 256, dtype=torch.bfloat16, device=DEV)
-    print(f"gemm_res_norm which={which} n={n}", flush=True)
-    _hip.gemm_res_norm(A.to(DEV), packed, which, Xd, xn)
+    print(f"gemm_res_norm {which} K={kd} n={n}", flush=True)
+    Wp = _hip.pack_weight(W.to(DEV))
+    _hip.gemm_res_norm(A.to(DEV), Wp, None if b is None else b.to(DEV), Xd, xn)
     torch.cuda.synchronize()
     torch.testing.assert_close(Xd.cpu(), Xr, rtol=1e-5, atol=1e-5)
     assert_bf16_close(xnr, xn, "xn", min_snr=55)
 
 
+@pytest.mark.parametrize("n_out", [1024, 96])
 @pytest.mark.parametrize("n", [1, 77, 4096])
-def test_gemm_gelu(hip, layers, n):
-    w, packed = layers[1]
+def test_gemm_gelu(hip, layers, n, n_out):
+    """gemm_gelu(xn, Wp, bias, H) with a standalone packed weight: FF1 (1024 outputs) and the first 96 rows
+    of it (the op takes any multiple of 32 outputs)."""
+    w, _ = layers[1]
+    W1, b1 = w["W1"][:n_out].contiguous(), w["b1"][:n_out].contiguous()
     xn = _xn(n, 50 + n)
-    Hr = ok.gemm_gelu(xn, w["W1"], w["b1"])
-    H = torch.empty(n, 1024, dtype=torch.bfloat16, device=DEV)
-    print(f"gemm_gelu n={n}", flush=True)
-    _hip.gemm_gelu(xn.to(DEV), packed, H)
+    Hr = ok.gemm_gelu(xn, W1, b1)
+    H = torch.empty(n, n_out, dtype=torch.bfloat16, device=DEV)
+    print(f"gemm_gelu n={n} n_out={n_out}", flush=True)
+    _hip.gemm_gelu(xn.to(DEV), _hip.pack_weight(W1.to(DEV)), b1.to(DEV), H)
     torch.cuda.synchronize()
     assert_bf16_close(Hr, H, "H", min_snr=50)
 

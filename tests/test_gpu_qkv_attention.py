@@ -99,3 +99,44 @@ def test_fused_short_attention_rejects_long_sequences(sharp_layers):
     assert lib.trf_qkv_attention_short(xn.data_ptr(), packed.data_ptr(), rope.data_ptr(), 1, 1, 2, 65,
                                        O.data_ptr(), None) == 1
     assert "at most 64" in lib.trf_last_error().decode()
+
+
+@pytest.mark.parametrize("F_big,fused", [(16912, True), (16913, False)])
+def test_time_sequences_with_a_large_token_stride(sharp_layers, F_big, fused):
+    """Time-mode sequences of 63 frames with a token stride of F = 16,912 / 16,913 bands.  The fused kernel
+    addresses a sequence's output rows with 32-bit buffer offsets and drops padded positions' stores at
+    byte 2^30; at F = 16,913 the sequence's rows ((62 F + 1) KB) would reach past that offset.  There the
+    per-op entry point refuses the shape and the block takes the unfused pair; at 16,912 both still take
+    the fused kernel.  Bands 0, 8,456 and F - 1 of the block's update are checked against the same bands
+    run alone (3 bands, the fused kernel): bitwise where both are fused, >= 55 dB (the fused kernel vs the
+    unfused pair) otherwise."""
+    w, packed = sharp_layers[0]
+    T, n = 63, 63 * F_big
+    rope = rope_table(w["freqs"], T).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(77)
+    X = torch.randn(n, 256, generator=g, device=DEV)
+    sel = torch.tensor([0, 8456, F_big - 1], device=DEV)
+    Xs = X.view(T, F_big, 256)[:, sel].reshape(-1, 256).contiguous()
+    x_in = Xs.clone()
+    print(f"large-stride time block T={T} F={F_big} fused={fused}", flush=True)
+    ws = torch.empty(_hip.workspace_bytes(1, T, F_big), dtype=torch.uint8, device=DEV)
+    _hip.attn_block(X, 1, T, F_big, packed, 0, rope, ws)
+    ws_s = torch.empty(_hip.workspace_bytes(1, T, 3), dtype=torch.uint8, device=DEV)
+    _hip.attn_block(Xs, 1, T, 3, packed, 0, rope, ws_s)
+    xn = torch.zeros(n, 256, dtype=torch.bfloat16, device=DEV)
+    O = torch.empty(n, 512, dtype=torch.bfloat16, device=DEV)
+    if fused:
+        _hip.qkv_attention_short(xn, packed, rope, 0, 1, T, F_big, O)
+    else:
+        with pytest.raises(RuntimeError, match="32-bit output offsets"):
+            _hip.qkv_attention_short(xn, packed, rope, 0, 1, T, F_big, O)
+    torch.cuda.synchronize()
+    big = X.view(T, F_big, 256)[:, sel].reshape(-1, 256)
+    assert torch.isfinite(big).all()
+    upd_big, upd_small = (big - x_in).double().cpu().numpy(), (Xs - x_in).double().cpu().numpy()
+    s = snr_db(upd_small, upd_big)
+    print(f"  update of bands {sel.tolist()} vs those bands alone: {s:.1f} dB")
+    if fused:
+        assert torch.equal(big, Xs)
+    else:
+        assert s >= 55.0

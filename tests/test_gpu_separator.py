@@ -7,7 +7,9 @@
   audio SNR against the oracle;
 * the 4:12 synthetic song with the full-size model and 17 s chunks (29 chunks, one batched stack
   forward of 29 x 62 sequences of 1701 frames): identical to the song run in batches of 4 chunks, finite,
-  and the schedule of the reference; the default batch, sized to the free device memory, covers the song;
+  and the schedule of the reference; its first chunk's mask and audio against the fp32 oracle forward of
+  that chunk (configuration 5's quality figure); the default batch, sized to the free device memory,
+  covers the song;
 * three threads sharing one Separator get the single-threaded result bit for bit (the reference's
   tests/test_separator.py:143-157), through ``separate`` and through ``forward_chunks`` on three streams.
 """
@@ -23,7 +25,7 @@ import torch
 
 from oracle import reference
 from turbo_roformer_amd import signals, weights
-from turbo_roformer_amd.chunking import overlap_add
+from turbo_roformer_amd.chunking import overlap_add, step_for
 from turbo_roformer_amd.separator import Separator
 
 from .conftest import snr_db
@@ -88,6 +90,48 @@ def test_full_song_batched(hip, full_sd):
     out4 = sep4.separate(x)
     assert snr_db(out, out4) >= 60.0
     assert 0.01 < float(np.abs(out).max()) < 10.0
+
+
+def test_full_song_batched_quality(hip, full_sd):
+    """Configuration 5's quality figure (the reference's --quality-seconds, benchmarks/bench_synthetic.py:
+    82-84): the 4:12 song separated as one batch of 29 chunks, its first chunk checked against the fp32
+    oracle forward of that chunk.  The batch's mask for chunk 0 >= 55 dB against the oracle's mask, the
+    batch's prediction for chunk 0 and the song's samples before chunk 1's start (covered by chunk 0
+    alone) >= 50 dB against the oracle's audio."""
+    cfg = weights.RESURRECTION_CFG
+    x = signals.song(252.0, seed=7)
+    sep = Separator(full_sd, cfg, 1701, "cuda", batch_chunks=0)
+    masks, preds = [], []
+    head, fwd = sep.mask_head, sep._forward_chunks
+
+    def mask_head(X, n_frames):
+        m = head(X, n_frames)
+        masks.append(m.float().cpu())
+        return m
+
+    def forward_chunks(chunks):
+        y = fwd(chunks)
+        preds.append(y.float().cpu())
+        return y
+
+    sep.mask_head, sep._forward_chunks = mask_head, forward_chunks
+    print("4:12 song, 29 chunks in one batch: chunk 0 against the fp32 oracle", flush=True)
+    out = sep.separate(x)
+    assert len(preds) == 1 and preds[0].shape[0] == 29, "one batch of 29 chunks"
+    T, width = 1701, masks[0].shape[1]
+    mask0 = masks[0].view(29, T, width)[0]
+    raw = torch.from_numpy(np.ascontiguousarray(x[:, : sep.chunk]))[None]  # chunk 0 starts at sample 0
+    Y = reference.stack(reference.stack_input(raw, full_sd, cfg), full_sd, cfg["depth"])
+    mask_ref = reference.mask_from_stack(Y, full_sd, cfg)
+    audio_ref = reference.apply_mask(raw, mask_ref, cfg)[0].numpy()
+    s_mask = snr_db(mask_ref[0].numpy(), mask0.numpy())
+    s_pred = snr_db(audio_ref, preds[0][0].numpy())
+    half = step_for(sep.chunk, 2.0)  # chunk 1's start
+    s_song = snr_db(audio_ref[:, :half], out[:, :half])
+    print(f"  chunk 0: mask {s_mask:.1f} dB, prediction {s_pred:.1f} dB, song's first {half} samples "
+          f"{s_song:.1f} dB vs fp32 oracle")
+    assert s_mask >= 55.0
+    assert s_pred >= 50.0 and s_song >= 50.0
 
 
 def test_full_model_dim_t_1700_matches_oracle(hip, full_sd):

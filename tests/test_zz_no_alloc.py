@@ -48,3 +48,30 @@ def test_static_workspace_rejects_shapes_beyond_it(full_stack):
     with pytest.raises(RuntimeError, match="static workspace"):
         _hip.stack_forward_static(X, 2, T, F, s.layers, s.modes, s.table(0, T), s.table(1, F), s.precision)
     assert bool((X == 0).all())  # rejected before any launch
+
+
+def test_static_workspace_forward_under_graph_capture(full_stack):
+    """The allocation-free entry point captured in a HIP graph (torch.cuda.CUDAGraph).  Its first call on a
+    device looks the static array's device address up, which has to happen outside a capture, so one eager
+    call comes first; the captured forward is then replayed three times, X restored and the stream
+    synchronised between replays, each bitwise equal to the eager forward."""
+    s = full_stack
+    T = 300
+    rt, rf = s.table(0, T), s.table(1, F)
+    X0 = _tokens(T, 3).to(DEV)
+    Xe = X0.clone()
+    print(f"static-workspace stack forward T={T}: eager, then captured and replayed", flush=True)
+    _hip.stack_forward_static(Xe, 1, T, F, s.layers, s.modes, rt, rf, s.precision)
+    torch.cuda.synchronize()
+    Xg = X0.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _hip.stack_forward_static(Xg, 1, T, F, s.layers, s.modes, rt, rf, s.precision)
+    torch.cuda.synchronize()
+    for r in range(3):
+        Xg.copy_(X0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"  replay {r}", flush=True)
+        assert torch.equal(Xg, Xe)

@@ -134,7 +134,7 @@ struct Events {
 // norm, and (with_ff) FF1 + GELU + FF2 + residual + norm in the same kernel.
 int run_layer(float* X, const trf::SeqShape& sh, const uint8_t* layer, const float* rope, const Workspace& w,
               int64_t n, bool with_ff, int ff_precision, hipStream_t st, const Events& ev = Events{}) {
-  if (sh.L <= 64) {
+  if (trf::fused_short_fits(sh)) {
     TRF_TRY(ev.empty(TRF_SLOT_QKV, st));
     trf::launch_qkv_attn_short(w.xn, layer, rope, sh, w.O, st, ev.of(TRF_SLOT_ATTN));
     TRF_TRY(check_launch("qkv_attention_short"));
@@ -409,6 +409,11 @@ int trf_qkv_attention_short(const uint16_t* xn, const void* packed_layer, const 
   if (int rc = check_shape(batch, T, F)) return rc;
   const trf::SeqShape sh = trf::seq_shape(mode, batch, T, F);
   if (sh.L > 64) return fail(TRF_ERR_ARG, "sequences of %d positions: the fused kernel takes at most 64", sh.L);
+  if (!trf::fused_short_fits(sh))
+    return fail(TRF_ERR_ARG,
+                "time-mode sequences of %d positions with token stride F = %d: the fused kernel's 32-bit output "
+                "offsets take at most %d bytes per sequence; use trf_qkv_rope_gemm + trf_attention",
+                sh.L, F, trf::kFusedShortDropped);
   TRF_REQUIRE(xn, "xn");
   TRF_REQUIRE(packed_layer, "packed_layer");
   TRF_REQUIRE(rope, "rope");
@@ -417,26 +422,44 @@ int trf_qkv_attention_short(const uint16_t* xn, const void* packed_layer, const 
   return check_launch("qkv_attention_short");
 }
 
-int trf_gemm_res_norm(const uint16_t* A, const void* packed_layer, int32_t which, float* X, uint16_t* xn,
+size_t trf_weight_packed_bytes(int32_t rows, int32_t K) {
+  if (rows < 1 || K < 16 || K % 16 != 0) return 0;
+  return size_t((rows + 31) / 32) * size_t(K / 16) * trf::kTileBytes;
+}
+
+int trf_pack_weight(const uint16_t* W, int32_t rows, int32_t K, void* packed, trf_stream_t stream) {
+  if (rows < 1 || K < 16 || K % 16 != 0)
+    return fail(TRF_ERR_ARG, "rows must be >= 1 and K a positive multiple of 16 (got %d, %d)", rows, K);
+  TRF_REQUIRE(W, "W");
+  TRF_REQUIRE(packed, "packed");
+  trf::launch_pack(W, rows, K, trf::kPack32Natural, static_cast<uint8_t*>(packed), as_hip(stream));
+  return check_launch("pack_weight");
+}
+
+int trf_gemm_res_norm(const uint16_t* A, int32_t K, const void* w_packed, const float* bias, float* X, uint16_t* xn,
                       int64_t n_rows, float eps, trf_stream_t stream) {
-  if (which != 0 && which != 1) return fail(TRF_ERR_ARG, "which must be 0 (out-proj) or 1 (ff2), got %d", which);
+  if (K < 16 || K % 16 != 0) return fail(TRF_ERR_ARG, "K must be a positive multiple of 16, got %d", K);
   TRF_REQUIRE(A, "A");
-  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(w_packed, "w_packed");
+  if (bias && !aligned(bias, 16)) return fail(TRF_ERR_ARG, "bias must be 16-byte aligned");
   TRF_REQUIRE(X, "X");
   TRF_REQUIRE(xn, "xn");
   if (n_rows < 0) return fail(TRF_ERR_ARG, "n_rows must be >= 0");
   if (n_rows == 0) return TRF_OK;
-  trf::launch_gemm_res_norm(A, static_cast<const uint8_t*>(packed_layer), which, X, xn, n_rows, eps, as_hip(stream));
+  trf::launch_gemm_res_norm(A, K, static_cast<const uint8_t*>(w_packed), bias, X, xn, n_rows, eps, as_hip(stream));
   return check_launch("gemm_res_norm");
 }
 
-int trf_gemm_gelu(const uint16_t* xn, const void* packed_layer, uint16_t* H, int64_t n_rows, trf_stream_t stream) {
+int trf_gemm_gelu(const uint16_t* xn, const void* w_packed, const float* bias, int32_t n_out, uint16_t* H,
+                  int64_t n_rows, trf_stream_t stream) {
+  if (n_out < 32 || n_out % 32 != 0) return fail(TRF_ERR_ARG, "n_out must be a positive multiple of 32, got %d", n_out);
   TRF_REQUIRE(xn, "xn");
-  TRF_REQUIRE(packed_layer, "packed_layer");
+  TRF_REQUIRE(w_packed, "w_packed");
+  TRF_REQUIRE(bias, "bias");
   TRF_REQUIRE(H, "H");
   if (n_rows < 0) return fail(TRF_ERR_ARG, "n_rows must be >= 0");
   if (n_rows == 0) return TRF_OK;
-  trf::launch_gemm_gelu(xn, static_cast<const uint8_t*>(packed_layer), H, n_rows, as_hip(stream));
+  trf::launch_gemm_gelu(xn, static_cast<const uint8_t*>(w_packed), bias, n_out, H, n_rows, as_hip(stream));
   return check_launch("gemm_gelu");
 }
 

@@ -71,6 +71,17 @@ inline SeqShape seq_shape(int mode, int batch, int T, int F) {
   return s;
 }
 
+// The fused short-sequence kernel (launch_qkv_attn_short) addresses a sequence's output rows (1 KB each,
+// token stride F in time mode, 1 in frequency mode) with 32-bit buffer offsets, and drops the stores of
+// padded positions by sending them to byte offset kFusedShortDropped, past every row of the sequence.  It
+// therefore takes a shape only when the sequence's last row ends below that offset; larger strides go
+// through the unfused pair (64-bit token indexing).
+constexpr int kFusedShortDropped = 1 << 30;
+inline bool fused_short_fits(const SeqShape& s) {
+  const int64_t stride = s.mode == 0 ? s.F : 1;
+  return s.L <= 64 && (int64_t(s.L - 1) * stride + 1) * kHeads * kHeadDim * 2 <= int64_t(kFusedShortDropped);
+}
+
 // Sets the calling thread's trf_last_error message (printf format) and returns code (trf_capi.hip).
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
@@ -99,9 +110,13 @@ void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, 
 // xn -> O with no Q/K/V/G buffers.  Requires sh.L <= 64.
 void launch_qkv_attn_short(const uint16_t* xn, const uint8_t* layer, const float* rope, const SeqShape& sh,
                            uint16_t* O, hipStream_t st, const LaunchEvents& ev = {});
-void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn,
-                          int64_t n, float eps, hipStream_t st);
-void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st);
+// Per-op GEMMs on a standalone weight packed by launch_pack in natural k order (kPack32Natural):
+// X += A [n][K] . W^T (+ bias), xn = X / max(|X|, eps) (W [256][K]); H = gelu_erf(xn . W^T + bias)
+// (W [n_out][256], n_out a multiple of 32).
+void launch_gemm_res_norm(const uint16_t* A, int K, const uint8_t* w_packed, const float* bias, float* X,
+                          uint16_t* xn, int64_t n, float eps, hipStream_t st);
+void launch_gemm_gelu(const uint16_t* xn, const uint8_t* w_packed, const float* bias, int n_out, uint16_t* H,
+                      int64_t n, hipStream_t st);
 // Fused out-projection + residual + norm [+ FF1 + GELU + FF2 + residual + norm]; ff_precision is a
 // FfPrecision value for the two FF GEMMs.
 void launch_post_attn(const uint16_t* O, const uint8_t* layer, float* X, uint16_t* xn, int64_t n, bool with_ff,

@@ -96,13 +96,6 @@ void launch_pack_f16(const uint16_t* hi, const uint16_t* lo, int rows, int K, ui
                      reinterpret_cast<u32x4*>(dst));
 }
 
-// B operand of a k-step read from an activation row in register order (see trf_internal.h).
-__device__ __forceinline__ u32x4 load_b_regorder(const uint16_t* row, int ks, int hh) {
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(row + 16 * ks + 4 * hh);
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16 * ks + 8 + 4 * hh);
-  return u32x4{lo[0], lo[1], hi[0], hi[1]};
-}
-
 __global__ void k_copy_f32(const float* __restrict__ src, int n, float* __restrict__ dst) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[i];
@@ -775,29 +768,28 @@ void launch_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, 
 }
 
 // ============================================================ GEMM + residual + next norm
-// X[tok] += A[tok] . W^T (+ b); xn[tok] = X / max(|X|, eps).  Each wave owns 32 tokens and all
-// 256 output features (8 accumulator tiles), so the row norm needs one half-wave swap.
+// X[tok] += A[tok] . W^T (+ b); xn[tok] = X / max(|X|, eps), for any A width K (a multiple of 16) and a
+// weight W [256][K] packed in natural k order (launch_pack, kPack32Natural).  Each wave owns 32 tokens
+// and all 256 output features (8 accumulator tiles), so the row norm needs one half-wave swap.
 // (kernels.cpp:542-586)
-template <int KD>
-__global__ __launch_bounds__(256) void k_gemm_res_norm(const uint16_t* __restrict__ A, const u32x4* __restrict__ wq,
-                                                       const float* __restrict__ bias, float* __restrict__ X,
-                                                       uint16_t* __restrict__ xn, int64_t n, float eps) {
-  constexpr int KS = KD / 16;
+__global__ __launch_bounds__(256) void k_gemm_res_norm(const uint16_t* __restrict__ A, int K,
+                                                       const u32x4* __restrict__ wq, const float* __restrict__ bias,
+                                                       float* __restrict__ X, uint16_t* __restrict__ xn, int64_t n,
+                                                       float eps) {
+  const int KS = K / 16;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int64_t tok0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
   if (tok0 >= n) return;
   const int64_t tok = tok0 + j;
   const bool valid = tok < n;
-  const u32x4* ar = reinterpret_cast<const u32x4*>(A + (valid ? tok : 0) * KD);
+  const u32x4* ar = reinterpret_cast<const u32x4*>(A + (valid ? tok : 0) * K);
 
   f32x16 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = zero16();
   for (int ks = 0; ks < KS; ++ks) {
-    // W_out is packed in natural k order, W2 in register order (see trf_internal.h)
-    u32x4 b = zero4();
-    if (valid) b = KD == 512 ? ar[2 * ks + hh] : load_b_regorder(A + tok * KD, ks, hh);
+    const u32x4 b = valid ? ar[2 * ks + hh] : zero4();  // A[tok][16ks + 8hh .. +7]
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = mfma32(wq[(int64_t(t) * KS + ks) * 64 + lane], b, acc[t]);
   }
@@ -834,36 +826,30 @@ __global__ __launch_bounds__(256) void k_gemm_res_norm(const uint16_t* __restric
     }
 }
 
-void launch_gemm_res_norm(const uint16_t* A, const uint8_t* layer, int which, float* X, uint16_t* xn, int64_t n,
-                          float eps, hipStream_t st) {
-  const unsigned blocks = unsigned((n + 127) / 128);
-  if (which == 0) {
-    hipLaunchKernelGGL(k_gemm_res_norm<512>, dim3(blocks), dim3(256), 0, st, A,
-                       reinterpret_cast<const u32x4*>(layer + kOffOut), static_cast<const float*>(nullptr), X, xn, n,
-                       eps);
-  } else {
-    hipLaunchKernelGGL(k_gemm_res_norm<1024>, dim3(blocks), dim3(256), 0, st, A,
-                       reinterpret_cast<const u32x4*>(layer + kOffFf2),
-                       reinterpret_cast<const float*>(layer + kOffBff2), X, xn, n, eps);
-  }
+void launch_gemm_res_norm(const uint16_t* A, int K, const uint8_t* w_packed, const float* bias, float* X,
+                          uint16_t* xn, int64_t n, float eps, hipStream_t st) {
+  hipLaunchKernelGGL(k_gemm_res_norm, dim3(unsigned((n + 127) / 128)), dim3(256), 0, st, A, K,
+                     reinterpret_cast<const u32x4*>(w_packed), bias, X, xn, n, eps);
 }
 
 // ============================================================ FF1 GEMM + GELU
-// H = 0.5 x (1 + erf(x / sqrt 2)), x = xn . W1^T + b1  (nn.GELU() default, model.py:69).
+// H = 0.5 x (1 + erf(x / sqrt 2)), x = xn . W^T + b  (nn.GELU() default, model.py:69), for a weight
+// W [n_out][256] packed in natural k order (n_out a multiple of 32) and H [n][n_out].
 __global__ __launch_bounds__(256) void k_gemm_gelu(const uint16_t* __restrict__ xn, const u32x4* __restrict__ wq,
-                                                   const float* __restrict__ b1, uint16_t* __restrict__ H,
-                                                   int64_t n) {
+                                                   const float* __restrict__ b1, int n_out,
+                                                   uint16_t* __restrict__ H, int64_t n) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int j = lane & 31, hh = lane >> 5;
   const int64_t tok0 = (int64_t(blockIdx.x) * 4 + wave) * 32;
   if (tok0 >= n) return;
   const int64_t tok = tok0 + j;
   const bool valid = tok < n;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(xn + (valid ? tok : 0) * kDim);
   u32x4 bx[16];
 #pragma unroll
-  for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? load_b_regorder(xn + tok * kDim, ks, hh) : zero4();  // W1: register order
-  uint16_t* hr = H + (valid ? tok : 0) * kHidden;
-  for (int t = 0; t < kHidden / 32; ++t) {
+  for (int ks = 0; ks < 16; ++ks) bx[ks] = valid ? xr[2 * ks + hh] : zero4();  // natural k order
+  uint16_t* hr = H + (valid ? tok : 0) * int64_t(n_out);
+  for (int t = 0; t < n_out / 32; ++t) {
     f32x16 acc = zero16();
     const u32x4* w = wq + int64_t(t) * 16 * 64 + lane;
 #pragma unroll
@@ -885,10 +871,10 @@ __global__ __launch_bounds__(256) void k_gemm_gelu(const uint16_t* __restrict__ 
   }
 }
 
-void launch_gemm_gelu(const uint16_t* xn, const uint8_t* layer, uint16_t* H, int64_t n, hipStream_t st) {
+void launch_gemm_gelu(const uint16_t* xn, const uint8_t* w_packed, const float* bias, int n_out, uint16_t* H,
+                      int64_t n, hipStream_t st) {
   hipLaunchKernelGGL(k_gemm_gelu, dim3(unsigned((n + 127) / 128)), dim3(256), 0, st, xn,
-                     reinterpret_cast<const u32x4*>(layer + kOffFf1), reinterpret_cast<const float*>(layer + kOffBff1),
-                     H, n);
+                     reinterpret_cast<const u32x4*>(w_packed), bias, n_out, H, n);
 }
 
 // ============================================================ fused post-attention block

@@ -54,7 +54,7 @@ constexpr int kFsOffB = kFsBlocksA * 64;
 constexpr int kFsOffKx = kFsOffB + kFsBlocksB * 64;
 constexpr int kFsOffVx = kFsOffKx + kFsSeqs * 2 * 4 * 64;
 constexpr int kFsLdsVecs = kFsOffVx + kFsSeqs * 2 * 4 * 64;
-constexpr int kFsDropped = 0x40000000;  // buffer offset past any sequence's output: the store is dropped
+constexpr int kFsDropped = kFusedShortDropped;  // buffer offset past any sequence's output: the store is dropped
 
 // This wave's share of the gate tile (the last tile of W_qkvg).
 __device__ __forceinline__ void fs_issue_gate(u32x4* buf, const u32x4* wq, int wave, int lane) {

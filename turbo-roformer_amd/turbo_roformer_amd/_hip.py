@@ -21,7 +21,7 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libtrf_hip.so")
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_hip.h"
-ABI_VERSION = 7
+ABI_VERSION = 8
 STATIC_WORKSPACE_BYTES = 512 << 20  # TRF_STATIC_WORKSPACE_BYTES of trf_hip.h
 
 DIM, HEADS, HEAD_DIM, QKVG_ROWS, FF_HIDDEN = 256, 8, 64, 1544, 1024
@@ -80,8 +80,10 @@ _SIGNATURES: dict[str, tuple] = {
     "trf_qkv_rope_gemm": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
     "trf_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
     "trf_qkv_attention_short": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P]),
-    "trf_gemm_res_norm": (ctypes.c_int, [_P, _P, _I32, _P, _P, _I64, _F, _P]),
-    "trf_gemm_gelu": (ctypes.c_int, [_P, _P, _P, _I64, _P]),
+    "trf_weight_packed_bytes": (_SZ, [_I32, _I32]),
+    "trf_pack_weight": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
+    "trf_gemm_res_norm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _F, _P]),
+    "trf_gemm_gelu": (ctypes.c_int, [_P, _P, _P, _I32, _P, _I64, _P]),
     "trf_stack_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "trf_stack_forward": (
         ctypes.c_int,
@@ -332,26 +334,54 @@ def qkv_attention_short(xn, layer, rope, mode, batch, T, F, O) -> None:
                                        O.data_ptr(), _stream()))
 
 
-def gemm_res_norm(A, layer, which, X, xn, eps: float = 1e-12) -> None:
-    """X += A W^T (+b); xn = X/|X| (kernels.cpp:542-586). which 0: out-proj (K=512), 1: FF2 (K=1024)."""
+def weight_packed_bytes(rows: int, K: int) -> int:
+    """Bytes of a weight [rows][K] packed by ``pack_weight``."""
+    return int(load().trf_weight_packed_bytes(rows, K))
+
+
+def pack_weight(W: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Pack a bf16 weight W [rows][K] (device) into the operand tiles the per-op GEMMs read: the
+    counterpart of ``_pack_w`` (fast.py:43-49) for ``gemm_res_norm`` / ``gemm_gelu``."""
     lib = load()
-    n = X.shape[0]
-    kd = 512 if which == 0 else FF_HIDDEN
-    _need(A, "A", torch.bfloat16, (n, kd))
-    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
+    if W.dim() != 2:
+        raise ValueError(f"W must be 2-D, got {tuple(W.shape)}")
+    rows, K = W.shape
+    nbytes = lib.trf_weight_packed_bytes(rows, K)
+    if nbytes == 0:
+        raise ValueError(f"W [{rows}][{K}]: K must be a positive multiple of 16")
+    _need(W, "W", torch.bfloat16, (rows, K))
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=W.device)
+    _need(out, "out", torch.uint8, (nbytes,))
+    _check(lib.trf_pack_weight(W.data_ptr(), rows, K, out.data_ptr(), _stream()))
+    return out
+
+
+def gemm_res_norm(A, Wp, bias, X, xn, eps: float = 1e-12) -> None:
+    """``gemm_res_norm(A, Wp, bias?, X, xn, eps)`` (kernels.cpp:542-586): X += A @ W^T (+ bias) and
+    xn = X / max(|X|, eps) as bf16, with W [256][K] packed by ``pack_weight``."""
+    lib = load()
+    n, K = A.shape
+    _need(A, "A", torch.bfloat16, (n, K))
+    _need(Wp, "Wp", torch.uint8, (lib.trf_weight_packed_bytes(DIM, K),))
+    if bias is not None:
+        _need(bias, "bias", torch.float32, (DIM,))
     _need(X, "X", torch.float32, (n, DIM))
     _need(xn, "xn", torch.bfloat16, (n, DIM))
-    _check(lib.trf_gemm_res_norm(A.data_ptr(), layer.data_ptr(), which, X.data_ptr(), xn.data_ptr(), n, eps, _stream()))
+    _check(lib.trf_gemm_res_norm(A.data_ptr(), K, Wp.data_ptr(), _ptr(bias), X.data_ptr(), xn.data_ptr(), n, eps,
+                                 _stream()))
 
 
-def gemm_gelu(xn, layer, H) -> None:
-    """H = gelu_erf(xn W1^T + b1) (kernels.cpp:609-642)."""
+def gemm_gelu(xn, Wp, bias, H) -> None:
+    """``gemm_gelu(xn, Wp, bias, H)`` (kernels.cpp:609-642): H = gelu_erf(xn @ W^T + bias) as bf16, with
+    W [n_out][256] packed by ``pack_weight``."""
     lib = load()
-    n = xn.shape[0]
+    n, n_out = H.shape
     _need(xn, "xn", torch.bfloat16, (n, DIM))
-    _need(layer, "layer", torch.uint8, (lib.trf_layer_packed_bytes(),))
-    _need(H, "H", torch.bfloat16, (n, FF_HIDDEN))
-    _check(lib.trf_gemm_gelu(xn.data_ptr(), layer.data_ptr(), H.data_ptr(), n, _stream()))
+    _need(Wp, "Wp", torch.uint8, (lib.trf_weight_packed_bytes(n_out, DIM),))
+    _need(bias, "bias", torch.float32, (n_out,))
+    _need(H, "H", torch.bfloat16, (n, n_out))
+    _check(lib.trf_gemm_gelu(xn.data_ptr(), Wp.data_ptr(), bias.data_ptr(), n_out, H.data_ptr(), n, _stream()))
 
 
 SLOTS = ("qkv_rope_gemm", "attention", "post_attention")  # trf_kernel_slot order
@@ -364,7 +394,7 @@ def stack_forward(X, batch, T, F, layers: list[torch.Tensor], modes: list[int], 
     ``precision``: ``"bf16"`` (every GEMM operand bf16, the reference kernels' arithmetic),
     ``"ff_fp16"`` (fp16 operands in the two FF GEMMs) or ``"ff_split"`` (split-bf16 operands there).
 
-    ``events``: optional list of 2*5*len(layers) ``torch.cuda.Event`` (or None) recorded before/after
+    ``events``: optional list of 2*len(SLOTS)*len(layers) ``torch.cuda.Event`` (or None) recorded before/after
     each kernel (slot order ``SLOTS``), for per-kernel timing on the launch stream."""
     lib = load()
     prec = precision_code(precision)
