@@ -132,6 +132,10 @@ def main() -> int:
                          "reference kernels")
     ap.add_argument("--no-alt-precisions", action="store_true",
                     help="time only --precision (the other two stack precisions are skipped)")
+    ap.add_argument("--mfma-peak", action="store_true",
+                    help="only run the MFMA-rate probe (libtrf_probe.so) and print its JSON line")
+    ap.add_argument("--hbm-probe", action="store_true",
+                    help="only run the HBM stream-bandwidth probe (libtrf_probe.so) and print its JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one plain 1 GiB device copy, the known-size reference for HBM counters")
     a = ap.parse_args()
@@ -139,6 +143,19 @@ def main() -> int:
         print("bench.py measures one GPU only: the stack runs on a single MI355X (no multi-GPU path is built)",
               file=sys.stderr)
         return 2
+
+    if a.mfma_peak or a.hbm_probe:
+        # the instruction-throughput and bandwidth figures the roofline fractions are read against (the
+        # reference's counterpart: benchmarks/dpbf16_peak.cpp)
+        from turbo_roformer_amd import probe
+
+        out = {"probe": "MI355X sustained rates", "device": torch.cuda.get_device_name(0)}
+        if a.mfma_peak:
+            out["mfma_bf16_32x32x16"] = probe.mfma_peak()
+        if a.hbm_probe:
+            out["hbm_stream"] = probe.hbm_stream()
+        print(json.dumps(out), flush=True)
+        return 0
 
     from turbo_roformer_amd import _hip, signals, weights
     from turbo_roformer_amd.band_split import HipBandSplit

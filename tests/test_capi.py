@@ -23,6 +23,19 @@ def test_exports_every_declared_function(lib):
     assert set(names) == set(_hip._SIGNATURES), "ctypes signatures out of sync with trf_hip.h"
 
 
+def test_probe_library_exports_every_declared_function():
+    from turbo_roformer_amd import probe
+
+    plib = probe.open_library()
+    names = probe.probe_functions()
+    assert names and all(hasattr(plib, n) for n in names)
+    assert set(names) == set(probe.SIGNATURES), "ctypes signatures out of sync with trf_probe.h"
+    p = ctypes.c_void_p(256)
+    assert plib.trf_probe_mfma_peak(3, 10, 1, p, None) == 1  # chains 1, 2, 4 or 8
+    assert plib.trf_probe_store(p, 1000, 0, 1, None) == 1  # not a multiple of 1 KB
+    assert plib.trf_probe_load(p, 1024, 2, 1, p, None) == 1  # pattern 0 or 1
+
+
 def test_version_and_sizes(lib):
     assert lib.trf_abi_version() == _hip.ABI_VERSION
     assert [lib.trf_seq_pad(L) for L in (1, 62, 64, 65, 1700, 1701)] == [64, 64, 64, 128, 1728, 1728]

@@ -1,0 +1,98 @@
+// Measurement probes for the roofline figures of the stack's kernels (libtrf_probe.so, include/trf_probe.h):
+// the sustained rate of v_mfma_f32_32x32x16_bf16 with register operands, and the HBM bandwidth of plain
+// streams of 16-byte loads or stores in two access patterns (whole 1 KB runs per instruction, and 64-byte
+// runs scattered across the buffer, the shape of the QKV kernel's V^T stores).  Nothing here is on the
+// stack's path.
+#include "trf_device.h"
+#include "trf_probe.h"
+
+namespace {
+
+using trf::f32x16;
+using trf::u32x4;
+
+// Each wave runs `chains` independent accumulator chains of `iters` MFMAs each, operands in registers.
+// The accumulators' sum leaves through out[wave] so the work cannot be dropped.
+template <int CHAINS>
+__global__ __launch_bounds__(256) void k_mfma_peak(int iters, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  u32x4 a = {0x3f803f80u ^ uint32_t(lane), 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  u32x4 b = {0x3c003c00u, 0x3c003c00u ^ uint32_t(lane), 0x3c003c00u, 0x3c003c00u};
+  f32x16 c[CHAINS];
+#pragma unroll
+  for (int i = 0; i < CHAINS; ++i) c[i] = trf::zero16();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < CHAINS; ++i) c[i] = trf::mfma32(a, b, c[i]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CHAINS; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += c[i][r];
+  if (lane == 0) out[blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)] = s;
+}
+
+// Element e (16 bytes) of a stream in pattern `scattered`: 0 keeps it in place (each wave instruction
+// covers 1 KB contiguous); 1 moves its 64-byte run r to run (r % 16) * (runs / 16) + r / 16, so the 16 runs
+// of one instruction land runs / 16 * 64 bytes apart (runs is a multiple of 16).
+__device__ __forceinline__ int64_t probe_element(int64_t e, int64_t runs, int scattered) {
+  if (!scattered) return e;
+  const int64_t r = e >> 2, rr = (r & 15) * (runs >> 4) + (r >> 4);
+  return (rr << 2) | (e & 3);
+}
+
+__global__ __launch_bounds__(256) void k_store_stream(u32x4* __restrict__ dst, int64_t n16, int scattered) {
+  const int64_t runs = n16 >> 2;
+  const u32x4 v = {uint32_t(threadIdx.x), 0u, 0u, 0u};
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n16; e += int64_t(gridDim.x) * blockDim.x)
+    dst[probe_element(e, runs, scattered)] = v;
+}
+
+__global__ __launch_bounds__(256) void k_load_stream(const u32x4* __restrict__ src, int64_t n16, int scattered,
+                                                     uint32_t* __restrict__ out) {
+  const int64_t runs = n16 >> 2;
+  uint32_t acc = 0;
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n16; e += int64_t(gridDim.x) * blockDim.x) {
+    const u32x4 v = src[probe_element(e, runs, scattered)];
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads; never true for the probe's data
+}
+
+int fail_hip(hipError_t e) { return e == hipSuccess ? 0 : 3; }
+
+}  // namespace
+
+extern "C" {
+
+int trf_probe_mfma_peak(int32_t chains, int32_t iters, int32_t workgroups, float* out, void* stream) {
+  if (iters < 1 || workgroups < 1 || !out) return 1;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (chains) {
+    case 1: hipLaunchKernelGGL(k_mfma_peak<1>, dim3(workgroups), dim3(256), 0, st, iters, out); break;
+    case 2: hipLaunchKernelGGL(k_mfma_peak<2>, dim3(workgroups), dim3(256), 0, st, iters, out); break;
+    case 4: hipLaunchKernelGGL(k_mfma_peak<4>, dim3(workgroups), dim3(256), 0, st, iters, out); break;
+    case 8: hipLaunchKernelGGL(k_mfma_peak<8>, dim3(workgroups), dim3(256), 0, st, iters, out); break;
+    default: return 1;
+  }
+  return fail_hip(hipGetLastError());
+}
+
+int trf_probe_store(void* dst, int64_t bytes, int32_t scattered, int32_t workgroups, void* stream) {
+  if (!dst || bytes <= 0 || bytes % 1024 != 0 || workgroups < 1 || (scattered != 0 && scattered != 1)) return 1;
+  hipLaunchKernelGGL(k_store_stream, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<u32x4*>(dst), bytes / 16, scattered);
+  return fail_hip(hipGetLastError());
+}
+
+int trf_probe_load(const void* src, int64_t bytes, int32_t scattered, int32_t workgroups, uint32_t* out,
+                   void* stream) {
+  if (!src || !out || bytes <= 0 || bytes % 1024 != 0 || workgroups < 1 || (scattered != 0 && scattered != 1))
+    return 1;
+  hipLaunchKernelGGL(k_load_stream, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src), bytes / 16, scattered, out);
+  return fail_hip(hipGetLastError());
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+"""Measurement probes (libtrf_probe.so, include/trf_probe.h): the sustained MFMA rate and HBM stream
+bandwidth that the kernels' roofline figures are read against.  The counterpart of the reference's
+instruction-throughput benchmark (benchmarks/dpbf16_peak.cpp); ``bench.py --mfma-peak --hbm-probe`` runs
+them.  Not on the stack's path."""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+from ._hip import HipUnavailable, header_functions
+
+LIB_PATH = Path(__file__).with_name("libtrf_probe.so")
+HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_probe.h"
+
+_P, _I32, _I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+SIGNATURES: dict[str, tuple] = {
+    "trf_probe_mfma_peak": (ctypes.c_int, [_I32, _I32, _I32, _P, _P]),
+    "trf_probe_store": (ctypes.c_int, [_P, _I64, _I32, _I32, _P]),
+    "trf_probe_load": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P]),
+}
+MFMA_FLOPS = 2 * 32 * 32 * 16  # one v_mfma_f32_32x32x16_bf16
+
+
+def probe_functions() -> list[str]:
+    return header_functions(HEADER_PATH)
+
+
+def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
+    if not path.exists():
+        raise HipUnavailable(f"{path.name} is not built (run `make -C turbo-roformer_amd/csrc`)")
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    return lib
+
+
+def _time(fn, reps: int, warmup: int) -> float:
+    """Mean ms of fn() over reps launches after warmup ones, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with code {rc}")
+
+
+def mfma_peak(iters: int = 20000, reps: int = 5, warmup: int = 20) -> dict:
+    """TFLOP/s of v_mfma_f32_32x32x16_bf16 on every SIMD: 1 or 2 waves per SIMD, 1-8 independent chains
+    per wave, register operands (no LDS or memory traffic)."""
+    lib = open_library()
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(2 * ncu * 4, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    res = {"cus": ncu, "iters": iters, "tflops": {}}
+    for waves_per_simd in (1, 2):
+        wg = waves_per_simd * ncu  # workgroups of 4 waves: one wave per SIMD each
+        for chains in (1, 2, 4, 8):
+            ms = _time(lambda: _check(lib.trf_probe_mfma_peak(chains, iters, wg, out.data_ptr(), st), "mfma probe"),
+                       reps, warmup)
+            flops = wg * 4 * chains * iters * MFMA_FLOPS
+            res["tflops"][f"{waves_per_simd}w_{chains}c"] = round(flops / (ms * 1e-3) / 1e12, 1)
+    res["best_tflops"] = max(res["tflops"].values())
+    return res
+
+
+def hbm_stream(nbytes: int = 1 << 30, reps: int = 10, warmup: int = 3) -> dict:
+    """GB/s of 16-byte load and store streams over nbytes: contiguous (1 KB per wave instruction) and
+    scattered 64-byte runs."""
+    lib = open_library()
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    wg = 16 * ncu
+    res = {"bytes": nbytes, "gbs": {}}
+    for scattered, name in ((0, "contiguous"), (1, "scattered_64B")):
+        ms = _time(lambda: _check(lib.trf_probe_store(buf.data_ptr(), nbytes, scattered, wg, st), "store probe"),
+                   reps, warmup)
+        res["gbs"][f"store_{name}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        ms = _time(lambda: _check(lib.trf_probe_load(buf.data_ptr(), nbytes, scattered, wg, sink.data_ptr(), st),
+                                  "load probe"), reps, warmup)
+        res["gbs"][f"load_{name}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    del buf
+    return res
