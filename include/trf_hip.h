@@ -9,10 +9,11 @@
  * kernels, and the steps either side of it: the band split that feeds the stack and the mask head
  * that follows it (fast.py:377-387), plus the overlap-add that assembles a song from its chunks.
  * Every entry point takes plain device pointers, sizes and a HIP stream;
- * no torch type appears in a signature.  The library allocates no memory and keeps
- * no state beyond a thread-local error string: the caller owns every buffer.  The one
- * exception is trf_stack_forward_static, whose workspace is a static device array the
- * library holds on each GPU it runs on (TRF_STATIC_WORKSPACE_BYTES).
+ * no torch type appears in a signature.  The library allocates no memory: the caller owns every
+ * buffer.  Its state is a thread-local error string, each device's CU count (read once, for the
+ * kernels that deal their work to one workgroup per CU) and the static workspace of
+ * trf_stack_forward_static: a device array of TRF_STATIC_WORKSPACE_BYTES in the library's code
+ * object, which every process that launches one of the library's kernels holds on that GPU.
  *
  * Shapes are fixed by the model: dim 256, 8 heads x 64, FF hidden 1024 (the mask head's
  * band widths and hidden size are arguments).

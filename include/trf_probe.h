@@ -21,10 +21,11 @@ extern "C" {
  * (device fp32, 4 * workgroups) receives one checksum per wave. */
 int trf_probe_mfma_peak(int32_t chains, int32_t iters, int32_t workgroups, float* out, void* stream);
 
-/* Writes `bytes` (a multiple of 1024) at dst with 16-byte stores: scattered = 0 as one stream (each wave
- * instruction 1 KB contiguous), 1 as 64-byte runs spread across the buffer (each instruction's 16 runs
- * bytes / 16 apart). */
-int trf_probe_store(void* dst, int64_t bytes, int32_t scattered, int32_t workgroups, void* stream);
+/* Writes `bytes` (a multiple of 1024) at dst with stores of `width` bytes per lane (16 or 8):
+ * scattered = 0 as one stream (each wave instruction 64 x width contiguous bytes), 1 as 64-byte runs
+ * spread across the buffer (an instruction's runs bytes / 16 apart). */
+int trf_probe_store(void* dst, int64_t bytes, int32_t scattered, int32_t width, int32_t workgroups,
+                    void* stream);
 
 /* Reads `bytes` at src with 16-byte loads in the same two patterns; out (device, 4 bytes) is only
  * written for one impossible checksum, so the loads are kept. */

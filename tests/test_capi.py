@@ -32,7 +32,8 @@ def test_probe_library_exports_every_declared_function():
     assert set(names) == set(probe.SIGNATURES), "ctypes signatures out of sync with trf_probe.h"
     p = ctypes.c_void_p(256)
     assert plib.trf_probe_mfma_peak(3, 10, 1, p, None) == 1  # chains 1, 2, 4 or 8
-    assert plib.trf_probe_store(p, 1000, 0, 1, None) == 1  # not a multiple of 1 KB
+    assert plib.trf_probe_store(p, 1000, 0, 16, 1, None) == 1  # not a multiple of 1 KB
+    assert plib.trf_probe_store(p, 1024, 0, 4, 1, None) == 1  # 16- or 8-byte stores
     assert plib.trf_probe_load(p, 1024, 2, 1, p, None) == 1  # pattern 0 or 1
 
 

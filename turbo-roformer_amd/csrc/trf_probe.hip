@@ -49,6 +49,21 @@ __global__ __launch_bounds__(256) void k_store_stream(u32x4* __restrict__ dst, i
     dst[probe_element(e, runs, scattered)] = v;
 }
 
+// The same streams with 8-byte stores: each wave instruction writes 512 contiguous bytes (pattern 0) or
+// eight 64-byte runs (pattern 1), the store width of the QKV kernel's outputs.
+__global__ __launch_bounds__(256) void k_store_stream8(trf::u32x2* __restrict__ dst, int64_t n8, int scattered) {
+  const int64_t runs = n8 >> 3;
+  const trf::u32x2 v = {uint32_t(threadIdx.x), 0u};
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n8; e += int64_t(gridDim.x) * blockDim.x) {
+    int64_t el = e;
+    if (scattered) {
+      const int64_t r = e >> 3, rr = (r & 15) * (runs >> 4) + (r >> 4);
+      el = (rr << 3) | (e & 7);
+    }
+    dst[el] = v;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_load_stream(const u32x4* __restrict__ src, int64_t n16, int scattered,
                                                      uint32_t* __restrict__ out) {
   const int64_t runs = n16 >> 2;
@@ -79,10 +94,16 @@ int trf_probe_mfma_peak(int32_t chains, int32_t iters, int32_t workgroups, float
   return fail_hip(hipGetLastError());
 }
 
-int trf_probe_store(void* dst, int64_t bytes, int32_t scattered, int32_t workgroups, void* stream) {
-  if (!dst || bytes <= 0 || bytes % 1024 != 0 || workgroups < 1 || (scattered != 0 && scattered != 1)) return 1;
-  hipLaunchKernelGGL(k_store_stream, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<u32x4*>(dst), bytes / 16, scattered);
+int trf_probe_store(void* dst, int64_t bytes, int32_t scattered, int32_t width, int32_t workgroups, void* stream) {
+  if (!dst || bytes <= 0 || bytes % 1024 != 0 || workgroups < 1 || (scattered != 0 && scattered != 1) ||
+      (width != 8 && width != 16))
+    return 1;
+  if (width == 16)
+    hipLaunchKernelGGL(k_store_stream, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<u32x4*>(dst), bytes / 16, scattered);
+  else
+    hipLaunchKernelGGL(k_store_stream8, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<trf::u32x2*>(dst), bytes / 8, scattered);
   return fail_hip(hipGetLastError());
 }
 

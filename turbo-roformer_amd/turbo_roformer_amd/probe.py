@@ -18,7 +18,7 @@ HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "trf_probe.h"
 _P, _I32, _I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
 SIGNATURES: dict[str, tuple] = {
     "trf_probe_mfma_peak": (ctypes.c_int, [_I32, _I32, _I32, _P, _P]),
-    "trf_probe_store": (ctypes.c_int, [_P, _I64, _I32, _I32, _P]),
+    "trf_probe_store": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P]),
     "trf_probe_load": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P]),
 }
 MFMA_FLOPS = 2 * 32 * 32 * 16  # one v_mfma_f32_32x32x16_bf16
@@ -77,7 +77,7 @@ def mfma_peak(iters: int = 20000, reps: int = 5, warmup: int = 20) -> dict:
 
 
 def hbm_stream(nbytes: int = 1 << 30, reps: int = 10, warmup: int = 3) -> dict:
-    """GB/s of 16-byte load and store streams over nbytes: contiguous (1 KB per wave instruction) and
+    """GB/s of load and store streams over nbytes (16-byte loads; 16- and 8-byte stores): contiguous and
     scattered 64-byte runs."""
     lib = open_library()
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
@@ -87,9 +87,10 @@ def hbm_stream(nbytes: int = 1 << 30, reps: int = 10, warmup: int = 3) -> dict:
     wg = 16 * ncu
     res = {"bytes": nbytes, "gbs": {}}
     for scattered, name in ((0, "contiguous"), (1, "scattered_64B")):
-        ms = _time(lambda: _check(lib.trf_probe_store(buf.data_ptr(), nbytes, scattered, wg, st), "store probe"),
-                   reps, warmup)
-        res["gbs"][f"store_{name}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        for width in (16, 8):
+            ms = _time(lambda: _check(lib.trf_probe_store(buf.data_ptr(), nbytes, scattered, width, wg, st),
+                                      "store probe"), reps, warmup)
+            res["gbs"][f"store{width}_{name}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         ms = _time(lambda: _check(lib.trf_probe_load(buf.data_ptr(), nbytes, scattered, wg, sink.data_ptr(), st),
                                   "load probe"), reps, warmup)
         res["gbs"][f"load_{name}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
