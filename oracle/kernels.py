@@ -93,9 +93,10 @@ def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int
     bf16, token order.
 
     ``shift="max"`` is the reference's shift m.  ``shift="device"`` follows the library: sequences of more
-    than 64 positions go through the single-sweep kernel, whose shift is an integer >= m; with an integer
-    shift P = 2^-c bf16(2^s), so every integer gives the same result and ceil(m) stands for it here.
-    Sequences of up to 64 positions keep m."""
+    than 64 positions go through the single-sweep kernel, whose shift is an integer >= m and whose
+    normaliser is the sum of the rounded P instead of e; with an integer shift P = 2^-c bf16(2^s), so
+    every integer gives the same result and ceil(m) stands for it here.  Sequences of up to 64 positions
+    keep m and the sum of e."""
     if shift not in ("device", "max"):
         raise ValueError("shift must be 'device' or 'max'")
     idx = token_index(mode, batch, T, F)
@@ -109,11 +110,13 @@ def attention(Q: Tensor, K: Tensor, Vt: Tensor, G: Tensor, mode: int, batch: int
         v = Vt[s0:s1, :, :, :L].double().transpose(-1, -2)
         S = (q @ k.transpose(-1, -2)).float()
         m = S.amax(dim=-1, keepdim=True)
-        if shift == "device" and L > 64:
+        single_sweep = shift == "device" and L > 64
+        if single_sweep:
             m = torch.ceil(m)
         e = torch.exp2(S - m)  # fp32
-        rs = e.double().sum(dim=-1, keepdim=True)
-        o = e.to(torch.bfloat16).double() @ v  # [s, H, L, DH]
+        P = e.to(torch.bfloat16).double()
+        rs = (P if single_sweep else e.double()).sum(dim=-1, keepdim=True)
+        o = P @ v  # [s, H, L, DH]
         tok = idx[s0:s1]  # [s, L]
         gate = G[tok].permute(0, 2, 1).unsqueeze(-1).double()  # [s, H, L, 1]
         o = (o * (gate / rs)).to(torch.bfloat16)

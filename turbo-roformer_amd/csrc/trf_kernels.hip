@@ -422,6 +422,46 @@ __device__ __forceinline__ void softmax_block(const f32x16& sacc, int key0, int 
   p1[3] = pk_bf16(e[14], e[15]);
 }
 
+// The same probabilities for the single-sweep kernel, whose normaliser is the sum of the bf16-rounded P
+// (the weights P.V actually applies), formed on the matrix pipe instead of by 16 VALU adds per block:
+// v_mfma_f32_16x16x32_bf16 with A = `ones` and B = the P^T operand.  B lane l is column n = l % 16 and
+// k-group l / 16; the P^T registers of lane l belong to query l % 32 = n + 16 ((l / 16) & 1), half
+// (l / 32) of the keys.  A row 0 is 1 on k-groups 0 and 2 and row 1 on k-groups 1 and 3, so D row 0,
+// column n (lane n, register 0) collects query n's 16 keys and row 1 (lane n, register 1) query n + 16's;
+// the other rows stay 0.
+__device__ __forceinline__ u32x4 rowsum_ones(int lane) {
+  const int m = lane & 15, g = (lane >> 4) & 1;
+  const uint32_t one = (m == 0 && g == 0) || (m == 1 && g == 1) ? 0x3f803f80u : 0u;
+  return u32x4{one, one, one, one};
+}
+
+__device__ __forceinline__ f32x4 mfma16_rowsum(u32x4 ones, u32x4 p, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, p), c,
+                                                 0, 0, 0);
+}
+
+__device__ __forceinline__ void softmax_block_psum(const f32x16& sacc, int key0, int L, int hh, const u32x4& ones,
+                                                   f32x4& psum, u32x4& p0, u32x4& p1) {
+  float e[16];
+  if (key0 + 32 <= L) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(sacc[r]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) e[r] = (key0 + key_of(r, hh) < L) ? __builtin_amdgcn_exp2f(sacc[r]) : 0.f;
+  }
+  p0 = u32x4{pk_bf16(e[0], e[1]), pk_bf16(e[2], e[3]), pk_bf16(e[4], e[5]), pk_bf16(e[6], e[7])};
+  p1 = u32x4{pk_bf16(e[8], e[9]), pk_bf16(e[10], e[11]), pk_bf16(e[12], e[13]), pk_bf16(e[14], e[15])};
+  psum = mfma16_rowsum(ones, p0, psum);
+  psum = mfma16_rowsum(ones, p1, psum);
+}
+
+// Query j's sum from the row-sum accumulator (j = lane % 32; both half-waves get it).
+__device__ __forceinline__ float psum_of_query(const f32x4& psum, int j) {
+  const float a = __shfl(psum[0], j & 15), b = __shfl(psum[1], j & 15);
+  return j < 16 ? a : b;
+}
+
 __device__ __forceinline__ float block_max(const f32x16& sacc, int key0, int L, int hh, float m) {
   if (key0 + 32 <= L) {
 #pragma unroll
@@ -461,6 +501,11 @@ __device__ __forceinline__ void attn_store(const f32x16 (&o)[2], int q, int L, i
 // shift changes neither the bf16 rounding of P nor the normalised result, QK^T is computed once instead of
 // twice, and no max is taken after the first keys; a workgroup whose sums overflow redoes the sweep with
 // a shift raised as scores exceed it.
+// The normaliser is the fp32 sum of the rounded P (on the matrix pipe, softmax_block_psum) rather than
+// of e.  With the row max the dominant key's P is exactly 1 and escapes bf16 rounding; with an integer
+// shift it is rounded like the others, and dividing by the sum of the weights P.V actually applied makes
+// up for that: against exact attention the result is within ~0.5 dB of the reference's arithmetic on
+// peaked rows, where the sum of e leaves it 2-3 dB below.
 // One workgroup = one (sequence, head) and 4 waves x 64 queries; each wave holds two 32-query column
 // tiles, so every K or V^T operand read from LDS feeds two MFMAs.  Tiles of 64 keys of K and V^T stream
 // through a ring of LDS buffers, loaded global->LDS directly (V^T with the XOR swizzle of its 16-byte
@@ -529,7 +574,8 @@ constexpr float kAttSafeSum = 1099511627776.0f;  // 2^40: fixed-shift sums at mo
 // from its own row max; SAFE (the guarded sweep) raises c when a score exceeds it.
 template <bool FIRST, bool MASK, bool SAFE>
 __device__ __forceinline__ void attn_half(const u32x4 (&ka)[4], const u32x4 (&qb)[4], int key0, int L, int hh,
-                                          f32x16& negc, float& lsum, f32x16 (&o)[2], u32x4& p0, u32x4& p1) {
+                                          const u32x4& ones, f32x16& negc, f32x4& psum, f32x16 (&o)[2], u32x4& p0,
+                                          u32x4& p1) {
   f32x16 sacc = FIRST ? zero16() : negc;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) sacc = mfma32(ka[ks], qb[ks], sacc);
@@ -553,20 +599,24 @@ __device__ __forceinline__ void attn_half(const u32x4 (&ka)[4], const u32x4 (&qb
       negc[r] -= d;
       sacc[r] -= d;
     }
-    lsum = ldexpf(lsum, -di);
+    // the row-sum accumulator of lane n < 16 holds queries n (register 0) and n + 16 (register 1)
+    const int di16 = __shfl(di, (__lane_id() & 15) + 16);
+    psum[0] = ldexpf(psum[0], -di);
+    psum[1] = ldexpf(psum[1], -di16);
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[dt][r] = ldexpf(o[dt][r], -di);
   }
-  softmax_block(sacc, MASK ? key0 : 0, MASK ? L : 32, hh, 0.0f, lsum, p0, p1);
+  softmax_block_psum(sacc, MASK ? key0 : 0, MASK ? L : 32, hh, ones, psum, p0, p1);
 }
 
 // One 64-key tile: per 32-key half, scores and probabilities for both query tiles, then P.V.
 template <bool FIRST, bool MASK, bool SAFE>
 __device__ __forceinline__ void attn_tile(const u32x4* __restrict__ Kl, const u32x4* __restrict__ Vl,
                                           const u32x4 (&qb)[kAttQT][4], int key0, int L, int j, int hh,
-                                          f32x16 (&negc)[kAttQT], float (&lsum)[kAttQT], f32x16 (&o)[kAttQT][2]) {
+                                          const u32x4& ones, f32x16 (&negc)[kAttQT], f32x4 (&psum)[kAttQT],
+                                          f32x16 (&o)[kAttQT][2]) {
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
     u32x4 ka[4];
@@ -575,9 +625,10 @@ __device__ __forceinline__ void attn_tile(const u32x4* __restrict__ Kl, const u3
 #pragma unroll
     for (int qt = 0; qt < kAttQT; ++qt) {
       if (FIRST && kh == 0)
-        attn_half<true, false, SAFE>(ka, qb[qt], 0, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
+        attn_half<true, false, SAFE>(ka, qb[qt], 0, L, hh, ones, negc[qt], psum[qt], o[qt], p0[qt], p1[qt]);
       else
-        attn_half<false, MASK, SAFE>(ka, qb[qt], key0 + 32 * kh, L, hh, negc[qt], lsum[qt], o[qt], p0[qt], p1[qt]);
+        attn_half<false, MASK, SAFE>(ka, qb[qt], key0 + 32 * kh, L, hh, ones, negc[qt], psum[qt], o[qt], p0[qt],
+                                     p1[qt]);
     }
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -628,13 +679,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   }
 
   const int nkt = Lpad / 64;  // >= 2: this kernel runs for L > 64
-  float lsum[kAttQT];
+  const u32x4 ones = rowsum_ones(lane);
+  f32x4 psum[kAttQT];
   f32x16 negc[kAttQT], o[kAttQT][2];
   auto sweep = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
     for (int qt = 0; qt < kAttQT; ++qt) {
-      lsum[qt] = 0.f;
+      psum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
       negc[qt] = o[qt][0] = o[qt][1] = zero16();
     }
 #pragma unroll
@@ -648,7 +700,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
       stage_k_tile(Kh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][0], wave, lane);
       stage_v_tile(Vh, kAttBufs - 1, Lpad, lds[kAttBufs - 1][1], wave, lane);
     }
-    if (active) attn_tile<true, false, SAFE>(lds[0][0], lds[0][1], qb, 0, L, j, hh, negc, lsum, o);
+    if (active) attn_tile<true, false, SAFE>(lds[0][0], lds[0][1], qb, 0, L, j, hh, ones, negc, psum, o);
     for (int kt = 1; kt < nkt - 1; ++kt) {
       if (kt + kAttBufs - 2 < nkt)  // K and V: 4 loads per younger tile in flight
         vmcnt_barrier<4 * (kAttBufs - 2)>();
@@ -660,12 +712,13 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
         stage_v_tile(Vh, kt + kAttBufs - 1, Lpad, lds[b][1], wave, lane);
       }
       if (active)
-        attn_tile<false, false, SAFE>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, negc, lsum, o);
+        attn_tile<false, false, SAFE>(lds[kt % kAttBufs][0], lds[kt % kAttBufs][1], qb, 0, L, j, hh, ones, negc,
+                                      psum, o);
     }
     vmcnt_barrier<0>();
     if (active)
       attn_tile<false, true, SAFE>(lds[(nkt - 1) % kAttBufs][0], lds[(nkt - 1) % kAttBufs][1], qb, (nkt - 1) * 64, L,
-                                   j, hh, negc, lsum, o);
+                                   j, hh, ones, negc, psum, o);
   };
   sweep(std::integral_constant<bool, false>{});
   // Overflow check of the fixed-shift sweep (a key far above the first ones): the guarded sweep again,
@@ -673,7 +726,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   bool bad = false;
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt) {
-    bad |= !(lsum[qt] + __shfl_xor(lsum[qt], 32) <= kAttSafeSum);
+    bad |= !(psum_of_query(psum[qt], j) <= kAttSafeSum);
     float om = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
@@ -685,7 +738,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_long(const uint16_t* __restrict
   if (!active) return;
 #pragma unroll
   for (int qt = 0; qt < kAttQT; ++qt)
-    attn_store(o[qt], q0 + 32 * qt + j, L, s, h, hh, mode, T, F, G, lsum[qt] + __shfl_xor(lsum[qt], 32), O);
+    attn_store(o[qt], q0 + 32 * qt + j, L, s, h, hh, mode, T, F, G, psum_of_query(psum[qt], j), O);
 }
 
 // Short sequences (frequency attention, L <= 64).  One wave = one (sequence, head): all
