@@ -136,6 +136,8 @@ def main() -> int:
                     help="only run the MFMA-rate probe (libtrf_probe.so) and print its JSON line")
     ap.add_argument("--hbm-probe", action="store_true",
                     help="only run the HBM stream-bandwidth probe (libtrf_probe.so) and print its JSON line")
+    ap.add_argument("--coissue-probe", action="store_true",
+                    help="only run the MFMA/VALU co-issue probe (libtrf_probe.so) and print its JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one plain 1 GiB device copy, the known-size reference for HBM counters")
     a = ap.parse_args()
@@ -144,7 +146,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    if a.mfma_peak or a.hbm_probe:
+    if a.mfma_peak or a.hbm_probe or a.coissue_probe:
         # the instruction-throughput and bandwidth figures the roofline fractions are read against (the
         # reference's counterpart: benchmarks/dpbf16_peak.cpp)
         from turbo_roformer_amd import probe
@@ -154,6 +156,8 @@ def main() -> int:
             out["mfma_bf16_32x32x16"] = probe.mfma_peak()
         if a.hbm_probe:
             out["hbm_stream"] = probe.hbm_stream()
+        if a.coissue_probe:
+            out["mfma_valu_coissue"] = probe.coissue()
         print(json.dumps(out), flush=True)
         return 0
 
