@@ -43,7 +43,9 @@ int trf_probe_load(const void* src, int64_t bytes, int32_t scattered, int32_t wo
  *   6 .. 10: one 64-key tile of the time-attention loop (two 32-query tiles, K and V^T operands from
  *            LDS): 6 with the row sum as fp32 adds of e, 7 with it on v_mfma_f32_16x16x32_bf16 (the
  *            kernel's form), 8 MFMAs only, 9 VALU only (exp2, adds, packs), 10 as 6 with exp2 replaced by
- *            a multiply. */
+ *            a multiply;
+ *   11, 12, 13: 8 operand blocks of 1 KB read from LDS (ds_read_b128) per iteration: 11 reads only,
+ *            12 each the A operand of one v_mfma_f32_32x32x16_bf16, 13 of two (two B operands). */
 int trf_probe_coissue(int32_t variant, int32_t iters, int32_t waves_per_simd, int32_t workgroups, float* out,
                       void* stream);
 

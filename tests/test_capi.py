@@ -35,7 +35,7 @@ def test_probe_library_exports_every_declared_function():
     assert plib.trf_probe_store(p, 1000, 0, 16, 1, None) == 1  # not a multiple of 1 KB
     assert plib.trf_probe_store(p, 1024, 0, 4, 1, None) == 1  # 16- or 8-byte stores
     assert plib.trf_probe_load(p, 1024, 2, 1, p, None) == 1  # pattern 0 or 1
-    assert plib.trf_probe_coissue(11, 10, 1, 1, p, None) == 1  # variants 0..10
+    assert plib.trf_probe_coissue(14, 10, 1, 1, p, None) == 1  # variants 0..13
     assert plib.trf_probe_coissue(0, 0, 1, 1, p, None) == 1  # at least one iteration
     assert plib.trf_probe_coissue(0, 10, 3, 1, p, None) == 1  # one or two waves per SIMD
 

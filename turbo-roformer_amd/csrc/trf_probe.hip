@@ -266,6 +266,48 @@ __global__ __launch_bounds__(512) void k_softmax_tile(int iters, float* __restri
   record(out, t0, sink);
 }
 
+// LDS operand streaming: per iteration every wave reads 8 operand blocks of 1 KB (ds_read_b128, 64 lanes
+// x 16 B, conflict-free) from a 32 KB table.  M = 0: reads only (one v_xor per block keeps them);
+// 1: each block is the A operand of one v_mfma_f32_32x32x16_bf16 (a GEMM whose waves hold one 32-column
+// tile); 2: of two MFMAs with different B operands (two column tiles per wave).
+template <int M>
+__global__ __launch_bounds__(512) void k_lds_stream(int iters, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  __shared__ u32x4 tab[32 * 64];
+  __shared__ float pad[kCoissuePadFloats - 32 * 64 * 4];
+  for (int i = threadIdx.x; i < 32 * 64; i += blockDim.x)
+    tab[i] = u32x4{0x3c003c00u ^ uint32_t(i & 0xff), 0x3c003c00u, 0x3c00bc00u, 0x3c003c00u ^ uint32_t(i >> 8)};
+  pad[threadIdx.x] = 1.0f;
+  __syncthreads();
+  const u32x4 b0 = {0x3c003c00u, 0x3c003c00u ^ uint32_t(lane), 0x3c003c00u, 0xbc003c00u};
+  const u32x4 b1 = {0x3c003c00u ^ uint32_t(lane), 0x3c003c00u, 0xbc003c00u, 0x3c003c00u};
+  f32x16 c[4], d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = d[i] = trf::zero16();
+  uint32_t bits = 0;
+  const int w = threadIdx.x >> 6;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+    const int base = ((it + w) & 3) * 8;  // 8 consecutive blocks of the table, rotating
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const u32x4 a = tab[(base + m) * 64 + lane];
+      if (M == 0) {
+        bits ^= a[0] ^ a[3];
+      } else {
+        c[m & 3] = trf::mfma32(a, b0, c[m & 3]);
+        if (M == 2) d[m & 3] = trf::mfma32(a, b1, d[m & 3]);
+      }
+    }
+  }
+  float sink = __uint_as_float(bits & 0x3f7fffffu) + pad[threadIdx.x];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sink += c[i][r] + d[i][r];
+  record(out, t0, sink);
+}
+
 int fail_hip(hipError_t e) { return e == hipSuccess ? 0 : 3; }
 
 }  // namespace
@@ -324,6 +366,9 @@ int trf_probe_coissue(int32_t variant, int32_t iters, int32_t waves_per_simd, in
     case 8: hipLaunchKernelGGL(k_softmax_tile<2>, g, b, 0, st, iters, out); break;
     case 9: hipLaunchKernelGGL(k_softmax_tile<3>, g, b, 0, st, iters, out); break;
     case 10: hipLaunchKernelGGL(k_softmax_tile<4>, g, b, 0, st, iters, out); break;
+    case 11: hipLaunchKernelGGL(k_lds_stream<0>, g, b, 0, st, iters, out); break;
+    case 12: hipLaunchKernelGGL(k_lds_stream<1>, g, b, 0, st, iters, out); break;
+    case 13: hipLaunchKernelGGL(k_lds_stream<2>, g, b, 0, st, iters, out); break;
     default: return 1;
   }
   return fail_hip(hipGetLastError());

@@ -117,6 +117,11 @@ SOFTMAX_TILE = (
     (9, "tile, VALU only"),
     (10, "tile, exp2 replaced by a multiply"),
 )
+LDS_STREAM = (
+    (11, "LDS 8 x 1 KB reads only"),
+    (12, "LDS 8 x 1 KB reads, 1 MFMA each"),
+    (13, "LDS 8 x 1 KB reads, 2 MFMAs each"),
+)
 
 
 def coissue(iters: int = 2000, reps: int = 3, warmup: int = 2) -> dict:
@@ -129,10 +134,10 @@ def coissue(iters: int = 2000, reps: int = 3, warmup: int = 2) -> dict:
     out = torch.zeros(2 * 8 * ncu, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     res = {"cus": ncu, "cycles_per_iteration": {}}
-    variants = [(v, n) for v, n, *_ in COISSUE_STREAMS] + list(SOFTMAX_TILE)
+    variants = [(v, n) for v, n, *_ in COISSUE_STREAMS] + list(SOFTMAX_TILE) + list(LDS_STREAM)
     for waves_per_simd in (1, 2):
         for v, name in variants:
-            it = iters * 4 if v < 6 else iters
+            it = iters * 4 if v < 6 or v > 10 else iters
             for _ in range(reps + warmup):
                 _check(lib.trf_probe_coissue(v, it, waves_per_simd, ncu, out.data_ptr(), st), "co-issue probe")
             torch.cuda.synchronize()
@@ -147,4 +152,7 @@ def coissue(iters: int = 2000, reps: int = 3, warmup: int = 2) -> dict:
     res["valu_issue_cycles_per_mfma"] = {
         name: round((c[f"2w {name}"] - 2 * valu) / (2 * nmfma), 1)
         for v, name, nmfma, pipe, valu in COISSUE_STREAMS if v in (2, 5)}
+    # LDS operand reads: 8 KB per wave and iteration, 4 or 8 waves per CU
+    res["lds_bytes_per_cycle_per_cu"] = {
+        f"{w}w {name}": round(8192 * 4 * w / c[f"{w}w {name}"], 1) for w in (1, 2) for v, name in LDS_STREAM}
     return res
