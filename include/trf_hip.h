@@ -139,12 +139,14 @@ int trf_qkv_rope_gemm(const uint16_t* xn, const void* packed_layer, const float*
                       float* G, trf_stream_t stream);
 
 /* Exact (non-online) softmax attention per (sequence, head): with s = q.k (q as written by
- * trf_qkv_rope_gemm), a shift c, P = bf16(2^(s - c)) unnormalised and the row sum of 2^(s - c) in
- * fp32, the epilogue writes
+ * trf_qkv_rope_gemm), a shift c, P = bf16(2^(s - c)) unnormalised and an fp32 row sum, the epilogue
+ * writes
  * O[tok][h*64 + d] = gate[tok][h] / rowsum * (P V)[.][d] in token order, bf16.
- * c is the row max m for sequences of up to 64 positions, as in the reference; longer sequences
- * are swept once with an integer c >= m (raised with exact power-of-two rescales), which gives the
- * same result as any integer shift and moves P's bf16 rounding by the factor 2^(m - ceil m).
+ * For sequences of up to 64 positions c is the row max m and the row sum is that of 2^(s - c), as in
+ * the reference.  Longer sequences are swept once with an integer c >= m (raised with exact
+ * power-of-two rescales), which gives the same result as any integer shift and moves P's bf16
+ * rounding by the factor 2^(m - ceil m); their row sum is that of the rounded P, which keeps the
+ * result as close to exact attention as the reference's row-max arithmetic.
  * Replaces attention (kernels.cpp:250-388). */
 int trf_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* Vt, const float* G,
                   uint16_t* O, int32_t mode, int32_t batch, int32_t T, int32_t F,
