@@ -134,20 +134,22 @@ def test_attention(hip, layers, mode, batch, T, F):
     assert snr_db(exact.view(n, 512).numpy(), O.double().cpu().numpy()) >= 40.0
 
 
-@pytest.mark.parametrize("T,F,key", [(900, 2, 700), (400, 64, 300)])
-def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers, T, F, key):
+@pytest.mark.parametrize("T,F,key,spiked", [(900, 2, 700, (96, 128)), (400, 64, 300, (96, 128)),
+                                            (900, 2, 700, (96, 112)), (900, 2, 700, (112, 128))])
+def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers, T, F, key, spiked):
     """Long sequences are swept with a fixed integer shift from the first 32 keys; a score far above it
-    overflows that sweep's sums, and the sweep is redone with the raised-shift method.  Here the 32 queries
-    96..127 of every (sequence, head) are a multiple of one key, so their scores on it are ~100 (base 2)
+    overflows that sweep's sums, and the sweep is redone with the raised-shift method.  Here the queries
+    `spiked` of every (sequence, head) are a multiple of one key, so their scores on it are ~100 (base 2)
     above the rest: the result must still be the softmax.  With F = 64, 512 of the 1,024 workgroups redo
-    their sweep."""
+    their sweep.  96..127 is one 32-query column tile; the half tiles 96..111 and 112..127 raise the
+    shift of queries j and j + 16 of a tile differently, whose row sums one lane holds together."""
     w, _ = layers[0]
     mode, batch = 0, 1
     n = batch * T * F
     xn = ok.l2_rows(rand_x(n, 77)).to(torch.bfloat16)
     Q, K, Vt, G = ok.qkv_rope(xn, w["W"], w["b_gate"], w["freqs"], mode, batch, T, F)
     K[:, :, :, key, :] = 4.0
-    Q[:, :, :, 96:128, :] = 100.0 / (64 * 16.0) * 4.0  # q . k_key = 64 * 4 * 0.39 = 100
+    Q[:, :, :, spiked[0]:spiked[1], :] = 100.0 / (64 * 16.0) * 4.0  # q . k_key = 64 * 4 * 0.39 = 100
     Oref = ok.attention(Q, K, Vt, G, mode, batch, T, F)
     O = torch.empty(n, 512, dtype=torch.bfloat16, device=DEV)
     print("attention with a dominant key (guarded sweep)", flush=True)
@@ -158,7 +160,7 @@ def test_attention_far_above_the_first_keys_takes_the_guarded_sweep(hip, layers,
     # the spiked queries attend to the one key alone: O = gate * V[key]
     idx = ok.token_index(mode, batch, T, F)  # [nseq, L] token of (sequence, position)
     for s_ in range(idx.shape[0]):
-        tok = idx[s_, 100]
+        tok = idx[s_, spiked[0] + 4]
         vk = Vt[s_, :, :, key].float()  # [8 heads, 64]
         want = (G[tok].float()[:, None] * vk).reshape(512)
         torch.testing.assert_close(O[tok].float().cpu(), want, rtol=1e-2, atol=1e-3)
