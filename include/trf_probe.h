@@ -36,7 +36,7 @@ int trf_probe_load(const void* src, int64_t bytes, int32_t scattered, int32_t wo
 /* `workgroups` workgroups (one per CU: each holds 96 KB of LDS) of 4 * waves_per_simd waves, so every
  * SIMD runs exactly waves_per_simd (1 or 2) waves; each wave runs `iters` iterations of one of these loops
  * and writes its cycle count (s_memtime) to out[2w] and a checksum to out[2w + 1] (device fp32,
- * 8 * waves_per_simd * workgroups):
+ * 8 * waves_per_simd * workgroups; the checksum only keeps the work alive and need not be finite):
  *   0, 1, 2: 8 v_mfma_f32_32x32x16_bf16 on four accumulator chains, each followed by 0, 4 or 8
  *            independent v_fma_f32, in that exact order (256 cycles of matrix pipe per iteration);
  *   3, 4, 5: 16 v_mfma_f32_16x16x32_bf16, each followed by 0, 2 or 4 v_fma_f32 (256 cycles as well);
